@@ -1,0 +1,173 @@
+/*
+ * liblbfq_hip.so -- C ABI of the MI355X (gfx950) fake-quant attention path.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and a HIP stream
+ * (hipStream_t passed as void*), launches asynchronously on that stream and
+ * returns 0 on success, -1 for an invalid argument and -2 for a launch
+ * failure; lbfq_last_error() returns the message of the last failure on the
+ * calling thread.  The library never allocates or frees device memory and
+ * never synchronises: the caller owns every input, output and workspace
+ * (the reference wrappers likewise allocate with torch.empty before each
+ * Triton launch, e.g. quant_triton.py:68-69, attention_triton.py:616-626).
+ *
+ * Tensor conventions: "NHD" is (B, S, H, D) contiguous, the reference's
+ * layout; "BHSD" is (B, H, S_pitch, D) and "BHDS" is (B, H, D, S_pitch), the
+ * head-major layouts the attention kernel streams.  dtype codes: 0 fp32,
+ * 1 fp16, 2 bf16.  FP8 is OCP E4M3FN stored as uint8.
+ *
+ * Citations are the reference interfaces each entry replaces (paths relative
+ * to the reference checkout src/low_bit_fake_quant/).
+ */
+#ifndef LBFQ_H
+#define LBFQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* lbfq_stream_t;
+
+/* ---- enums ---------------------------------------------------------------- */
+enum { LBFQ_F32 = 0, LBFQ_F16 = 1, LBFQ_BF16 = 2 };
+enum { LBFQ_SUB_NONE = 0, LBFQ_SUB_COLVEC = 1, LBFQ_SUB_BLOCKVEC = 2 };
+enum {
+  LBFQ_Q_NONE = 0,          /* transform (+gather/smooth/Hadamard) only          */
+  LBFQ_Q_FP8_BLOCK = 1,     /* one FP32 scale per R-row tile of one head        */
+  LBFQ_Q_CHANNEL = 2,       /* scale per (b,h,d) = amax_table / 448             */
+  LBFQ_Q_MX_QK = 3,         /* power-of-two scale per (row, 32 columns)         */
+  LBFQ_Q_MX_V = 4,          /* power-of-two scale per (R-row tile, column)      */
+  LBFQ_Q_CHANNEL_AMAX = 5   /* atomic max of |x| per (b,h,d) into amax_table    */
+};
+enum { LBFQ_LAYOUT_NHD = 0, LBFQ_LAYOUT_BHSD = 1, LBFQ_LAYOUT_BHDS = 2 };
+enum { LBFQ_DQ_BLOCK = 0, LBFQ_DQ_CHANNEL = 1, LBFQ_DQ_MX_QK = 2, LBFQ_DQ_MX_V = 3 };
+
+const char* lbfq_last_error(void);
+
+/* ---- prepass: row-tile transform + quantisation ---------------------------
+ * Replaces the quantisers quant_triton.py:61-77 (fp8_block_quant), :163-176
+ * (fp8_per_channel_quant, with LBFQ_Q_CHANNEL_AMAX then LBFQ_Q_CHANNEL),
+ * :255-271 (mxfp8_qk_quant), :354-369 (mxfp8_v_quant); the smoothing
+ * writers preprocess.py:38-57, :135-166, :169-193 (subtract a mean, write
+ * the work tensor); the Hadamard rotation hadamard.py:77-117; and the
+ * reorder gathers kmeans.py:88-89 / :127-135 (gather != NULL).
+ * Per element: x[gather[s]] - sub -> round to x_dtype -> (signs, FWHT,
+ * *had_scale, round) -> quantise.  One tile = R rows of one (b, h). */
+typedef struct {
+  const void* x; int x_dtype;              /* input, NHD                        */
+  int64_t B, S, H, D;                      /* D in {64, 128}                    */
+  int R;                                   /* tile rows (quant block along S)   */
+  const int32_t* gather;                   /* (B*H, S) source rows or NULL      */
+  int sub_mode; const float* sub;          /* COLVEC (B,H,D) / BLOCKVEC (B,S/G,H,D) */
+  int sub_block;                           /* G for BLOCKVEC                    */
+  void* smoothed;                          /* optional NHD output in x_dtype    */
+  int hadamard; const int8_t* signs;       /* signs (H, D) +-1 or NULL          */
+  float had_scale;                         /* fp32(1/sqrt(D))                   */
+  int quant_mode;                          /* LBFQ_Q_*                          */
+  uint8_t* codes; int codes_layout;        /* LBFQ_LAYOUT_*                     */
+  int64_t codes_spitch;                    /* S extent of BHSD/BHDS buffers     */
+  float* scale;                            /* scale output (see strides)        */
+  int64_t sc_b, sc_s, sc_h, sc_d;          /* element strides of scale          */
+  uint32_t* amax_table;                    /* (B,H,D) fp32 bits, channel modes  */
+  int mx_block;                            /* MX-QK columns per scale (8..D)    */
+  int smoothed_stage;                      /* 0: after subtract, 1: after FWHT  */
+} lbfq_rowtile_params;
+
+int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream);
+
+/* Sequential fp64 column sums over `chunk`-row chunks (optionally gathered):
+ * mode 0 -> partial (B, nchunk, H, D) fp64; mode 1 -> mean fp32 per chunk.
+ * Replaces the reductions of preprocess.py:10-36 (smooth_k, mode 0 +
+ * lbfq_colsum_finalize), :60-91 (group_mean_q, mode 1, chunk = block_q) and
+ * :94-132 (smooth_v_per_block, mode 1, chunk = block_s). */
+int lbfq_colsum(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int chunk,
+                const int32_t* gather, int mode, double* partial, float* mean, lbfq_stream_t stream);
+int lbfq_colsum_finalize(const double* partial, int64_t B, int64_t nchunk, int64_t H, int64_t D,
+                         int64_t S, float* mean, lbfq_stream_t stream);
+
+/* Fill n uint32 words (initialises the channel amax table to bits(1e-4f)). */
+int lbfq_fill_u32(uint32_t* p, int64_t n, uint32_t value, lbfq_stream_t stream);
+
+/* FP8 dequantisation of NHD codes to out_dtype: quant_triton.py:111-131
+ * (BLOCK), :200-218 (CHANNEL), :300-319 (MX_QK, block = block_d),
+ * :398-416 (MX_V, block = block_s). */
+int lbfq_dequant(const uint8_t* codes, const float* scale, int64_t B, int64_t S, int64_t H, int64_t D,
+                 int mode, int block, void* out, int out_dtype, lbfq_stream_t stream);
+
+/* ---- k-means token reorder (replaces flash-kmeans batch_kmeans_Euclid as
+ * called at kmeans.py:78-81 and the argsort/scatter at kmeans.py:84-87) ----
+ * x: NHD tensor; per (b, h) slice cluster S tokens of dimension D into K
+ * clusters with `iters` Lloyd rounds (deterministic init from `seed`).
+ * Workspace: centroids (B*H, K, D) fp32, partial (B*H, ceil(S/1024), K, D)
+ * fp64, counts (B*H, ceil(S/1024), K) int32.  Outputs labels / order /
+ * inverse as (B*H, S) int32. */
+int64_t lbfq_kmeans_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t D, int K);
+int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int K, int iters,
+                uint64_t seed, void* workspace, int32_t* labels, int32_t* order, int32_t* inverse,
+                lbfq_stream_t stream);
+
+/* ---- qm_k row-max estimate + qm correction table --------------------------
+ * Replaces attention.py:366-395 (_estimate_rowmax_from_qm_k) and precomputes
+ * the kernel's qm correction attention_triton.py:156-160:
+ *   bias[b,h,g,n]   = (qm[b,g,h,:] . K_s[b,n,h,:]) * sm_scale   (fp32)
+ *   rowmax[b,h,g]   = max_n bias[b,h,g,n]
+ * K_s is NHD (dtype) optionally gathered by `gather` (V-kmeans order).
+ * bias is (B,H,G,s_pitch) (NULL to skip), rowmax (B,H,G) (NULL to skip). */
+int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, int64_t B, int64_t S,
+             int64_t H, int64_t D, int64_t G, float sm_scale, float* bias, int64_t s_pitch, float* rowmax,
+             lbfq_stream_t stream);
+
+/* ---- FP8-MFMA P-requant attention ------------------------------------------
+ * Replaces fake_quant_attention_triton (attention_triton.py:410-671) and its
+ * kernel _fake_quant_attn_fwd_kernel (attention_triton.py:48-407), taking
+ * FP8 codes + scales instead of pre-dequantised bf16 tensors. */
+typedef struct {
+  int64_t B, H, S, D;             /* S queries == S keys; D in {64, 128}          */
+  int64_t s_pitch;                /* rows of the code buffers, multiple of 128     */
+  const uint8_t* q_codes;         /* (B,H,s_pitch,D)                               */
+  const uint8_t* k_codes;         /* (B,H,s_pitch,D)                               */
+  const uint8_t* v_codes_t;       /* (B,H,D,s_pitch)                               */
+  int qk_mx;                      /* 0: fp8_block scales, 1: MX (block 32 along D) */
+  const float* q_scale;           /* fp8_block: [b*sb + (s/qk_block)*ss + h*sh]    */
+  const float* k_scale;           /* mx: [b*sb + s*ss + h*sh + (d/32)*sd]          */
+  int64_t qsc_b, qsc_s, qsc_h, qsc_d;
+  int64_t ksc_b, ksc_s, ksc_h, ksc_d;
+  int qk_block;                   /* fp8_block rows per scale (multiple of 16)     */
+  int v_kind;                     /* 0 channel (B,H,D), 1 block (B,S/vb,H), 2 mx (B,S/vb,H,D) */
+  const float* v_scale;
+  int v_block;                    /* rows per V scale (kinds 1, 2; multiple of 64) */
+  int p_mode;                     /* 0 elementwise, 1 mx, 2 dynamic               */
+  float sm_scale;
+  int p_max_offset;
+  int block_m;                    /* BLASST stats granularity (multiple of 32)     */
+  const float* qk_bias;           /* (B,H,G,s_pitch) natural units, or NULL        */
+  int q_group;                    /* rows per qm group (multiple of 32)            */
+  const float* rowmax_est;        /* per-group (B,H,G) natural units, or NULL       */
+  int rowmax_dynamic;             /* 1: qm_k thresholds (dynamic P), 0: fixed m    */
+  const float* v_alpha;           /* (B,S/vsb,H,D) fp32 or NULL                    */
+  int v_smooth_block;             /* multiple of 64                                */
+  float blasst_lambda;            /* <= 0 disables BLASST                          */
+  int blasst_fill;                /* 0 zero,1 max,2 mean,3 logn,4 sample8,5 thr,6 uta */
+  float blasst_fill_alpha;
+  int blasst_uta_bins;
+  float* blasst_stats;            /* (ceil(S/block_m), B*H, 2) fp32, zeroed, or NULL */
+  void* out; int out_dtype;       /* NHD (B,S,H,D)                                 */
+  const int32_t* out_row_map;     /* (B*H, S): output row of reordered query, or NULL */
+} lbfq_attn_params;
+
+int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t stream);
+
+/* ---- building-block self tests (GPU unit tests of compiler builtins) ------ */
+/* E4M3 conversion of n fp32 values (n even) by the hardware converter. */
+int lbfq_selftest_cvt_fp8(const float* x, int64_t n, uint8_t* out, lbfq_stream_t stream);
+/* One 32x32x64 FP8 MFMA per wave: A (32x64), B (64x32) E4M3 row-major,
+ * optional E8M0 scales per (row, 32-col block) of A and per (col, 32-row
+ * block) of B; C (32x32) fp32 row-major. */
+int lbfq_selftest_mfma(const uint8_t* a, const uint8_t* b, const uint8_t* a_scale, const uint8_t* b_scale,
+                       float* c, lbfq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LBFQ_H */

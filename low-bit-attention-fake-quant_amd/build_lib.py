@@ -1,0 +1,65 @@
+"""Compile liblbfq_hip.so (all HIP kernels + the C ABI) for gfx950.
+
+Each ``csrc/*.hip`` translation unit is compiled with hipcc into an object,
+then linked into ``low_bit_fake_quant/liblbfq_hip.so`` (in-tree, next to the
+Python package that loads it).  The prepass / k-means translation units are
+compiled with ``-ffp-contract=off`` so their arithmetic is exactly the
+documented op sequence (the CPU oracle reproduces it bit for bit); the
+attention unit allows contraction.  Packed-FP32 instructions are disabled
+for all device code.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "low_bit_fake_quant", "liblbfq_hip.so")
+BUILD = os.path.join(HERE, "_build")
+ARCH = os.environ.get("LBFQ_ARCH", "gfx950")
+
+COMMON = [
+    "hipcc", f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+UNITS = {
+    "lbfq_prepass.hip": ["-ffp-contract=off"],
+    "lbfq_kmeans.hip": ["-ffp-contract=off"],
+    "lbfq_qmk.hip": ["-ffp-contract=off"],
+    "lbfq_attn.hip": [],
+}
+
+
+def _compile(unit: str, extra: list[str]) -> str:
+    src = os.path.join(CSRC, unit)
+    obj = os.path.join(BUILD, unit.replace(".hip", ".o"))
+    cmd = COMMON + extra + ["-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {unit}:\n{' '.join(cmd)}\n{r.stderr}")
+    return obj
+
+
+def build(verbose: bool = True) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=len(UNITS)) as ex:
+        objs = list(ex.map(lambda kv: _compile(*kv), UNITS.items()))
+    tmp = OUT + ".tmp"
+    cmd = ["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stderr}")
+    os.replace(tmp, OUT)
+    if verbose:
+        print(f"built {OUT}", file=sys.stderr)
+    return OUT
+
+
+if __name__ == "__main__":
+    build()

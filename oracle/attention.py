@@ -1,0 +1,309 @@
+"""CPU restatement of the P-requant attention kernel (test infrastructure only).
+
+``attention`` follows the K-loop of ``_fake_quant_attn_fwd_kernel``
+(``attention_triton.py:109-407``) and the guards / fill parsing of
+``fake_quant_attention_triton`` (``attention_triton.py:463-714``); rows are
+processed all at once (rows are independent in that kernel) and the loop
+runs over K-blocks of ``block_n`` exactly as the reference does:
+
+* scores ``s = (q_deq . k_deq) * sm_scale`` in fp32, plus the qm correction
+  ``(qm[group] . K_smooth) * sm_scale`` (lines 154-160); masked columns -inf;
+* row max: online (215-217), ``qm_k`` estimate with the dynamic-P
+  up/down thresholds 16/32 (log2 units) or the fixed estimate (176-214),
+  BLASST predicate (165-175);
+* ``p = exp2((s - m) * log2e [+ p_max_offset for elementwise])`` (219-230);
+* BLASST fills zero/max/mean/logn/sample8/thr/uta (231-324);
+* ``l = l * alpha + sum(p)`` on the pre-quant p (326);
+* P quant elementwise / mx / dynamic (329-360);
+* ``pv = p_deq @ v``, fp8_block V scale per block (363-372), ``acc`` and the
+  V-smoothing accumulator (376-383);
+* epilogue ``(acc * v_scale[d] | acc) (+ c) / l`` (387-402) and BLASST stats
+  per ``block_m`` rows (404-407).
+
+Tensors are BHSD torch CPU tensors; q/k are the bf16 dequantised values, v is
+FP8 values held in bf16 (fp8_channel / fp8_block) or the pre-dequantised
+bf16 V (mxfp8), exactly as the reference marshals them
+(``attention.py:554-575``).  ``rows`` restricts the computation to a subset
+of query rows (used for the bounded CPU baseline sample).
+
+Pinned by ``tests/test_oracle_attention.py``: against a dense brute-force
+softmax at tiny S (online row max, P quant off-by-construction cases), the
+reference tests' own torch mirrors restated (``tests/test_triton_attn.py``
+of the reference), mx-P independence of ``p_max_offset`` (bitwise), qm_k vs
+online agreement for dynamic P, V-smoothing accumulator == un-smoothed V.
+"""
+
+from __future__ import annotations
+
+import math
+import re
+
+import numpy as np
+import torch
+
+from . import fp8
+from .quant import ceil_log2_exact
+
+LOG2E = 1.4426950408889634
+FP8_MAX = 448.0
+
+FILL_ZERO, FILL_MAX, FILL_MEAN, FILL_LOGN, FILL_SAMPLE8, FILL_THR, FILL_UTA = range(7)
+
+
+def parse_blasst_fill(mode, *, alpha: float, uta_bins: int):
+    """``attention_triton.py:674-714``."""
+    if mode is None or mode == "zero":
+        return FILL_ZERO, float(alpha), 1
+    if mode == "max":
+        return FILL_MAX, float(alpha), 1
+    if mode.startswith("max_a"):
+        return FILL_MAX, float(mode[len("max_a"):]), 1
+    if mode == "mean":
+        return FILL_MEAN, float(alpha), 1
+    if mode.startswith("mean_a"):
+        return FILL_MEAN, float(mode[len("mean_a"):]), 1
+    if mode == "logn":
+        return FILL_LOGN, float(alpha), 1
+    if mode == "sample8":
+        return FILL_SAMPLE8, float(alpha), 1
+    if mode.startswith("sample8_a"):
+        return FILL_SAMPLE8, float(mode[len("sample8_a"):]), 1
+    if mode == "thr":
+        return FILL_THR, float(alpha), 1
+    if mode.startswith("thr_a"):
+        return FILL_THR, float(mode[len("thr_a"):]), 1
+    if mode == "uta":
+        if uta_bins <= 0:
+            raise ValueError(f"blasst_uta_bins must be > 0; got {uta_bins}")
+        return FILL_UTA, float(alpha), int(uta_bins)
+    m = re.fullmatch(r"uta(\d+)(?:_a([0-9]+(?:\.[0-9]+)?))?", mode)
+    if m:
+        bins = int(m.group(1))
+        if bins <= 0:
+            raise ValueError(f"UTA bin count must be > 0; got {bins}")
+        a = float(m.group(2)) if m.group(2) is not None else float(alpha)
+        return FILL_UTA, a, bins
+    raise ValueError(f"unknown blasst_fill_mode: {mode!r}")
+
+
+def _e4m3_sat(x: torch.Tensor) -> torch.Tensor:
+    return torch.from_numpy(fp8.round_to_e4m3(x.contiguous().numpy()))
+
+
+def _f32(x: float) -> torch.Tensor:
+    return torch.tensor(x, dtype=torch.float32)
+
+
+def estimate_rowmax_qm_k(qm: torch.Tensor, k_work: torch.Tensor, *, block_q: int, sm_scale: float) -> torch.Tensor:
+    """``attention.py:366-395``: (B,H,S) fp32 = max_n(qm[g] . K_s[n]) * sm_scale."""
+    qm_b = qm.permute(0, 2, 1, 3).float()                 # (B,H,G,D)
+    k_b = k_work.permute(0, 2, 1, 3).float()              # (B,H,S,D)
+    g = torch.matmul(qm_b, k_b.transpose(-2, -1)).amax(dim=-1)
+    return (g * _f32(sm_scale)).repeat_interleave(block_q, dim=2).contiguous()
+
+
+def attention(q, k, v, v_scale, *, sm_scale, p_max_offset, block_m=64, block_n=64,
+              v_alpha=None, v_smooth_block=0, k_smooth=None, qm=None, q_smooth_block=0,
+              v_block_scale=None, v_block_size=0, p_quant_mode="elementwise",
+              rowmax_est=None, rowmax_init=None, blasst_lambda=None, blasst_fill_mode="zero",
+              blasst_fill_alpha=1.0, blasst_uta_bins=16, return_blasst_stats=False,
+              rows=None, return_debug=False):
+    B, H, S, D = q.shape
+    dev_rows = torch.arange(S) if rows is None else torch.as_tensor(rows)
+    R = dev_rows.numel()
+    qf = q.float()[:, :, dev_rows]
+    kf = k.float()
+    vf = v.float()
+    sm = _f32(sm_scale)
+
+    p_kind = {"elementwise": 0, "mx": 1, "dynamic": 2}[p_quant_mode]
+    use_blasst = blasst_lambda is not None
+    if use_blasst:
+        if not (0.0 < float(blasst_lambda) < 1.0):
+            raise ValueError(f"blasst_lambda must be in (0, 1); got {blasst_lambda}")
+        log_lam = math.log(float(blasst_lambda))
+        fill_kind, fill_alpha, uta_bins = parse_blasst_fill(blasst_fill_mode, alpha=blasst_fill_alpha,
+                                                            uta_bins=blasst_uta_bins)
+        if fill_kind == FILL_UTA and block_n % uta_bins:
+            raise ValueError(f"blasst UTA bins ({uta_bins}) must divide block_n ({block_n})")
+    has_qm = qm is not None
+    if has_qm:
+        qm_rows = qm.permute(0, 2, 1, 3).float()[:, :, dev_rows // q_smooth_block]   # (B,H,R,D)
+        ks = k_smooth.float()
+    if rowmax_est is not None:
+        rme = rowmax_est.float()[:, :, dev_rows]
+        m_i = rme.clone()
+    elif rowmax_init is not None:
+        rme = rowmax_init.float()[:, :, dev_rows]
+        m_i = rme.clone()
+    else:
+        rme = torch.zeros(B, H, R)
+        m_i = torch.full((B, H, R), -math.inf)
+    l_i = torch.zeros(B, H, R)
+    acc = torch.zeros(B, H, R, D)
+    c_acc = torch.zeros(B, H, R, D)
+    max_seen = torch.full((B, H, R), -math.inf)
+    skipped = torch.zeros(B, H, R)
+    total = torch.zeros(B, H, R)
+    row_valid = (dev_rows < S).float()
+    dbg = {"skip": []} if return_debug else None
+
+    for start_n in range(0, S, block_n):
+        n1 = min(start_n + block_n, S)
+        nb = n1 - start_n
+        col_mask = torch.zeros(block_n, dtype=torch.bool)
+        col_mask[:nb] = True
+        kb = torch.zeros(B, H, block_n, D)
+        kb[:, :, :nb] = kf[:, :, start_n:n1]
+        vb = torch.zeros(B, H, block_n, D)
+        vb[:, :, :nb] = vf[:, :, start_n:n1]
+        s = torch.matmul(qf, kb.transpose(-2, -1)) * sm
+        if has_qm:
+            ksb = torch.zeros(B, H, block_n, D)
+            ksb[:, :, :nb] = ks[:, :, start_n:n1]
+            corr = torch.matmul(qm_rows, ksb.transpose(-2, -1)) * sm
+            s = s + corr
+        s = torch.where(col_mask, s, torch.tensor(-math.inf))
+
+        skip = torch.zeros(B, H, R, dtype=torch.bool)
+        if use_blasst:
+            block_max = s.amax(-1)
+            m_ij = torch.maximum(m_i, block_max)
+            skip = (block_max - m_ij) < log_lam
+            alpha = torch.exp2((m_i - m_ij) * LOG2E)
+            alpha = torch.where(skip, torch.ones_like(alpha), alpha)
+            m_ij = torch.where(skip, m_i, m_ij)
+            skipped += skip.float()
+            total += row_valid
+        elif rowmax_est is not None:
+            if p_kind == 2:
+                block_max = s.amax(-1)
+                max_seen_ij = torch.maximum(max_seen, block_max)
+                up_t = 16.0 / LOG2E
+                down_t = 32.0 / LOG2E
+                under = (block_max - m_i) > up_t
+                over = (m_i - max_seen_ij) > down_t
+                adjust = under | over
+                down_b = torch.maximum(max_seen_ij + down_t, m_i - 80.0)
+                down_m = torch.where(l_i == 0.0, max_seen_ij, down_b)
+                adj_m = torch.where(under, block_max, down_m)
+                m_ij = torch.where(adjust, adj_m, m_i)
+                alpha_u = torch.exp2((m_i - m_ij) * LOG2E)
+                alpha_u = torch.where(l_i == 0.0, torch.zeros_like(alpha_u), alpha_u)
+                alpha = torch.where(adjust, alpha_u, torch.ones_like(alpha_u))
+                max_seen = max_seen_ij
+            else:
+                m_ij = rme
+                alpha = torch.ones(B, H, R)
+        else:
+            m_ij = torch.maximum(m_i, s.amax(-1))
+            alpha = torch.exp2((m_i - m_ij) * LOG2E)
+
+        if p_kind == 0:
+            z = (s - m_ij[..., None]) * LOG2E + float(p_max_offset)
+        else:
+            z = (s - m_ij[..., None]) * LOG2E
+        p = torch.exp2(z)
+        p = torch.where(col_mask, p, torch.zeros_like(p))
+
+        if use_blasst:
+            if fill_kind == FILL_ZERO:
+                p = torch.where(skip[..., None], torch.zeros_like(p), p)
+            else:
+                p_exact = torch.where(skip[..., None], torch.zeros_like(p), p)
+                safe_n = float(max(nb, 1))
+                fill_offset = float(p_max_offset) if p_kind == 0 else 0.0
+                s_stat = torch.where(col_mask, s, torch.zeros_like(s))
+                mean = s_stat.sum(-1) / safe_n
+                max_bound = safe_n * torch.exp2((block_max - m_ij) * LOG2E + fill_offset)
+                p_fill = torch.zeros_like(p)
+                sel = skip[..., None] & col_mask
+                if fill_kind == FILL_MAX:
+                    fill_p = max_bound * fill_alpha / safe_n
+                    p_fill = torch.where(sel, fill_p[..., None], p_fill)
+                elif fill_kind == FILL_MEAN:
+                    mass = fill_alpha * safe_n * torch.exp2((mean - m_ij) * LOG2E + fill_offset)
+                    mass = torch.minimum(mass, max_bound)
+                    p_fill = torch.where(sel, (mass / safe_n)[..., None], p_fill)
+                elif fill_kind == FILL_LOGN:
+                    centered = torch.where(col_mask, s - mean[..., None], torch.zeros_like(s))
+                    var = (centered * centered).sum(-1) / safe_n
+                    mass = safe_n * torch.exp2((mean + 0.5 * var - m_ij) * LOG2E + fill_offset)
+                    mass = torch.minimum(mass, max_bound)
+                    p_fill = torch.where(sel, (mass / safe_n)[..., None], p_fill)
+                elif fill_kind == FILL_SAMPLE8:
+                    stride = block_n // 8 if block_n >= 8 else 1
+                    rel = torch.arange(block_n)
+                    smask = ((rel % stride) == 0) & col_mask
+                    cnt = float(max(int(smask.sum()), 1))
+                    sp = torch.exp2((s - m_ij[..., None]) * LOG2E + fill_offset)
+                    sp = torch.where(smask, sp, torch.zeros_like(sp))
+                    mass = fill_alpha * safe_n * sp.sum(-1) / cnt
+                    mass = torch.minimum(mass, max_bound)
+                    p_fill = torch.where(sel, (mass / safe_n)[..., None], p_fill)
+                elif fill_kind == FILL_THR:
+                    off_scale = 2.0 ** float(p_max_offset) if p_kind == 0 else 1.0
+                    mass = fill_alpha * safe_n * float(blasst_lambda) * off_scale
+                    p_fill = torch.where(sel, torch.full_like(p, mass / safe_n), p_fill)
+                else:
+                    rel = torch.arange(block_n)
+                    bsz = block_n // uta_bins
+                    for bi in range(uta_bins):
+                        bmask = (rel >= bi * bsz) & (rel < (bi + 1) * bsz) & col_mask
+                        bc = float(max(int(bmask.sum()), 1))
+                        bmean = torch.where(bmask, s, torch.zeros_like(s)).sum(-1) / bc
+                        bmax = torch.where(bmask, s, torch.full_like(s, -math.inf)).amax(-1)
+                        bound = bc * torch.exp2((bmax - m_ij) * LOG2E + fill_offset)
+                        mass = fill_alpha * bc * torch.exp2((bmean - m_ij) * LOG2E + fill_offset)
+                        mass = torch.minimum(mass, bound)
+                        p_fill = torch.where(skip[..., None] & bmask, (mass / bc)[..., None], p_fill)
+                p = p_exact + p_fill
+            if dbg is not None:
+                dbg["skip"].append(skip.clone())
+
+        l_i = l_i * alpha + p.sum(-1)
+
+        if p_kind == 0:
+            p_deq = _e4m3_sat(p).to(torch.bfloat16).float()
+        elif p_kind == 1:
+            ra = p.abs().amax(-1).clamp_min(float(np.float32(1e-4)))
+            e = np.clip(ceil_log2_exact((ra / _f32(FP8_MAX)).numpy()), -127, 127)
+            sP = torch.from_numpy(np.ldexp(np.float32(1.0), e).astype(np.float32))
+            ps = torch.clamp(p / sP[..., None], -FP8_MAX, FP8_MAX)
+            p_deq = (_e4m3_sat(ps) * sP[..., None]).to(torch.bfloat16).float()
+        else:
+            ra = p.abs().amax(-1).clamp_min(float(np.float32(1e-12)))
+            sP = ra / _f32(FP8_MAX)
+            ps = torch.clamp(p / sP[..., None], -FP8_MAX, FP8_MAX)
+            p_deq = (_e4m3_sat(ps) * sP[..., None]).to(torch.bfloat16).float()
+
+        pv = torch.matmul(p_deq, vb)
+        if v_block_scale is not None:
+            svb = v_block_scale.float()[:, start_n // v_block_size, :]     # (B, H)
+            pv = pv * svb[..., None, None]
+        acc = acc * alpha[..., None] + pv
+        if v_alpha is not None:
+            av = v_alpha.float()[:, start_n // v_smooth_block]             # (B, H, D)
+            rs = p_deq.sum(-1)
+            c_acc = c_acc * alpha[..., None] + rs[..., None] * av[:, :, None, :]
+        m_i = m_ij
+
+    inv_l = 1.0 / l_i[..., None]
+    out_main = acc if v_block_scale is not None else acc * v_scale.float()[:, :, None, :]
+    out = (out_main + c_acc) * inv_l if v_alpha is not None else out_main * inv_l
+    out = out.to(torch.bfloat16)
+    result = [out]
+    if return_blasst_stats:
+        nblk = (S + block_m - 1) // block_m
+        st = torch.zeros(nblk, B * H, 2)
+        blk = dev_rows // block_m
+        sk = skipped.reshape(B * H, R)
+        tt = total.reshape(B * H, R)
+        for bi in range(nblk):
+            sel = blk == bi
+            st[bi, :, 0] = sk[:, sel].sum(-1)
+            st[bi, :, 1] = tt[:, sel].sum(-1)
+        result.append(st)
+    if dbg is not None:
+        result.append(dbg)
+    return result[0] if len(result) == 1 else tuple(result)

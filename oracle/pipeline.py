@@ -1,0 +1,210 @@
+"""CPU restatement of ``fake_quant_attention`` end to end (test infrastructure only).
+
+Follows ``attention.py`` of the reference:
+
+* ``preprocess``           -- ``attention.py:166-239`` (Q k-means, K smoothing,
+                              Q group mean, V k-means + K co-permute, V smoothing);
+* ``quant_qk_deq``         -- ``attention.py:89-121, 531-535`` (optional Hadamard
+                              on the quantiser inputs, quant, dequant to bf16);
+* ``p_requant_path``       -- ``attention.py:505-639`` (V kind marshalling,
+                              rowmax estimate, P mode, kernel call);
+* ``sdpa_path``            -- ``attention.py:247-321``;
+* ``fake_quant_attention`` -- ``attention.py:706-806`` (guards, inverse Q gather).
+
+``cfg`` is any object with the ``QuantConfig`` fields.  All tensors are CPU.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import attention as oattn
+from . import hadamard as ohad
+from . import kmeans as okm
+from . import preprocess as opre
+from . import quant as oq
+
+
+def preprocess(q, k, v, cfg):
+    q_work, k_work, v_work = q.contiguous(), k.contiguous(), v.contiguous()
+    q_km = None
+    if cfg.q_kmeans_k is not None:
+        q_km = okm.kmeans_reorder_tokens(q_work, n_clusters=cfg.q_kmeans_k,
+                                         max_iters=cfg.q_kmeans_iters, seed=cfg.q_kmeans_seed)
+        q_work = q_km["tensor_reordered"]
+    qm = None
+    if cfg.smoothing == "off":
+        pass
+    elif cfg.smoothing == "k_only":
+        k_work, _ = opre.smooth_k(k_work)
+    elif cfg.smoothing == "full":
+        k_work, _ = opre.smooth_k(k_work)
+        q_work, qm = opre.group_mean_q(q_work, block_q=cfg.q_smooth_block_size)
+    else:
+        raise ValueError(f"unsupported smoothing: {cfg.smoothing!r}")
+    v_km = None
+    if cfg.v_kmeans_k is not None:
+        v_km = okm.kmeans_reorder_tokens(v_work, n_clusters=cfg.v_kmeans_k,
+                                         max_iters=cfg.v_kmeans_iters, seed=cfg.v_kmeans_seed)
+        v_work = v_km["tensor_reordered"]
+        k_work = okm.apply_kv_permutation(k_work, v_km["order"])
+    v_alpha = None
+    if cfg.v_smooth_mode == "per_block":
+        v_work, v_alpha = opre.smooth_v_per_block(v_work, block_s=cfg.v_smooth_block_size)
+    elif cfg.v_smooth_mode != "off":
+        raise ValueError(f"unsupported v_smooth_mode: {cfg.v_smooth_mode!r}")
+    return q_work, k_work, v_work, qm, v_alpha, q_km, v_km
+
+
+def quant_qk(t, cfg):
+    if cfg.qk_quant == "fp8_block":
+        c, s = oq.fp8_block_quant(t, cfg.fp8_block_size)
+        return c, s, ("fp8_block", cfg.fp8_block_size)
+    if cfg.qk_quant == "mxfp8":
+        c, s = oq.mxfp8_qk_quant(t, cfg.mxfp8_block_size)
+        return c, s, ("mxfp8", cfg.mxfp8_block_size)
+    raise ValueError(f"unsupported qk_quant: {cfg.qk_quant!r}")
+
+
+def dequant_qk(c, s, meta, dtype):
+    if meta[0] == "fp8_block":
+        return oq.fp8_block_dequant(c, s, meta[1], dtype=dtype)
+    return oq.mxfp8_qk_dequant(c, s, meta[1], dtype=dtype)
+
+
+def quant_v(t, cfg):
+    if cfg.v_quant == "fp8_channel":
+        c, s = oq.fp8_per_channel_quant(t)
+        return c, s, ("fp8_channel", 0)
+    if cfg.v_quant == "fp8_block":
+        c, s = oq.fp8_block_quant(t, cfg.v_fp8_block_size)
+        return c, s, ("fp8_block", cfg.v_fp8_block_size)
+    if cfg.v_quant == "mxfp8":
+        c, s = oq.mxfp8_v_quant(t, cfg.v_mxfp8_block_size)
+        return c, s, ("mxfp8", cfg.v_mxfp8_block_size)
+    raise ValueError(f"unsupported v_quant: {cfg.v_quant!r}")
+
+
+def dequant_v(c, s, meta, dtype):
+    if meta[0] == "fp8_channel":
+        return oq.fp8_per_channel_dequant(c, s, dtype=dtype)
+    if meta[0] == "fp8_block":
+        return oq.fp8_block_dequant(c, s, meta[1], dtype=dtype)
+    return oq.mxfp8_v_dequant(c, s, meta[1], dtype=dtype)
+
+
+def qk_quant_inputs(q_work, k_work, cfg):
+    if not cfg.qk_hadamard:
+        return q_work, k_work
+    return ohad.apply_qk_hadamard(q_work, k_work, random_sign=cfg.qk_hadamard_random_sign,
+                                  seed=cfg.qk_hadamard_seed)
+
+
+def p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype, rows=None,
+                   return_blasst_stats=False):
+    b, s, h, d = q_work.shape
+    qi, ki = qk_quant_inputs(q_work, k_work, cfg)
+    qc, qs, qmeta = quant_qk(qi, cfg)
+    kc, ks, kmeta = quant_qk(ki, cfg)
+    q_deq = dequant_qk(qc, qs, qmeta, torch.bfloat16)
+    k_deq = dequant_qk(kc, ks, kmeta, torch.bfloat16)
+    vc, vs, vmeta = quant_v(v_work, cfg)
+    v_block_scale, v_block_size = None, 0
+    if vmeta[0] == "fp8_channel":
+        v_bf = oq.decode(vc).to(torch.bfloat16)
+        v_scale = vs.float()
+    elif vmeta[0] == "fp8_block":
+        v_bf = oq.decode(vc).to(torch.bfloat16)
+        v_scale = torch.ones(b, h, d)
+        v_block_scale, v_block_size = vs.float(), vmeta[1]
+    else:
+        v_bf = dequant_v(vc, vs, vmeta, torch.bfloat16)
+        v_scale = torch.ones(b, h, d)
+    perm = (0, 2, 1, 3)
+    k_smooth = qm_arg = None
+    if qm is not None:
+        k_smooth = k_work.to(torch.bfloat16).permute(*perm).contiguous()
+        qm_arg = qm.float()
+    rowmax_est = None
+    if cfg.rowmax_mode == "qm_k":
+        if qm is None:
+            raise ValueError("rowmax_mode='qm_k' requires smoothing='full' so qm exists")
+        rowmax_est = oattn.estimate_rowmax_qm_k(qm, k_work, block_q=cfg.q_smooth_block_size,
+                                                sm_scale=sm_scale)
+    elif cfg.rowmax_mode != "online":
+        raise ValueError(f"unsupported rowmax_mode: {cfg.rowmax_mode!r}")
+    p_mode = cfg.p_quant
+    if p_mode == "auto":
+        p_mode = "mx" if vmeta[0] == "mxfp8" else "elementwise"
+    res = oattn.attention(
+        q_deq.permute(*perm).contiguous(), k_deq.permute(*perm).contiguous(),
+        v_bf.permute(*perm).contiguous(), v_scale,
+        sm_scale=sm_scale, p_max_offset=int(cfg.p_max_offset),
+        block_m=cfg.p_requant_block_m, block_n=cfg.p_requant_block_n,
+        v_alpha=v_alpha, v_smooth_block=cfg.v_smooth_block_size if v_alpha is not None else 0,
+        k_smooth=k_smooth, qm=qm_arg, q_smooth_block=cfg.q_smooth_block_size if qm is not None else 0,
+        v_block_scale=v_block_scale, v_block_size=v_block_size, p_quant_mode=p_mode,
+        rowmax_est=rowmax_est, blasst_lambda=cfg.blasst_lambda, blasst_fill_mode=cfg.blasst_fill,
+        blasst_fill_alpha=cfg.blasst_fill_alpha, blasst_uta_bins=cfg.blasst_uta_bins,
+        return_blasst_stats=return_blasst_stats, rows=rows)
+    if return_blasst_stats:
+        o, st = res
+        return o.permute(*perm).contiguous().to(out_dtype), st
+    return res.permute(*perm).contiguous().to(out_dtype)
+
+
+def sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype):
+    b, s, h, d = q_work.shape
+    qi, ki = qk_quant_inputs(q_work, k_work, cfg)
+    qc, qs, qmeta = quant_qk(qi, cfg)
+    kc, ks, kmeta = quant_qk(ki, cfg)
+    vc, vs, vmeta = quant_v(v_work, cfg)
+    q_deq = dequant_qk(qc, qs, qmeta, sdpa_dtype)
+    k_deq = dequant_qk(kc, ks, kmeta, sdpa_dtype)
+    v_deq = dequant_v(vc, vs, vmeta, sdpa_dtype)
+    if v_alpha is not None:
+        v_deq = v_deq + v_alpha.repeat_interleave(cfg.v_smooth_block_size, dim=1).to(sdpa_dtype)
+    perm = (0, 2, 1, 3)
+    if qm is None:
+        o = F.scaled_dot_product_attention(q_deq.permute(*perm).float(), k_deq.permute(*perm).float(),
+                                           v_deq.permute(*perm).float(), scale=sm_scale)
+        return o.to(sdpa_dtype).permute(*perm).contiguous()
+    block_q = cfg.q_smooth_block_size
+    qb = q_deq.permute(*perm).float()
+    qmb = qm.permute(*perm).float()
+    kb = k_deq.permute(*perm).float()
+    ksb = k_work.permute(*perm).float()
+    vb = v_deq.permute(*perm).float()
+    grp = torch.arange(s) // block_q
+    s_main = torch.matmul(qb, kb.transpose(-2, -1)) * sm_scale
+    s_corr = torch.matmul(qmb[:, :, grp], ksb.transpose(-2, -1)) * sm_scale
+    p = torch.softmax(s_main + s_corr, dim=-1).to(sdpa_dtype).float()
+    return torch.matmul(p, vb).to(sdpa_dtype).permute(*perm).contiguous()
+
+
+def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=False):
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q/k/v shapes must match")
+    out_dtype = q.dtype
+    sdpa_dtype = torch.float16 if out_dtype == torch.float16 else torch.bfloat16
+    b, s, h, d = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    if cfg.blasst_lambda is not None and not cfg.p_requant:
+        raise ValueError("BLASST skip/fill requires cfg.p_requant=True")
+    q_work, k_work, v_work, qm, v_alpha, q_km, _ = preprocess(q, k, v, cfg)
+    stats = None
+    if cfg.p_requant:
+        r = p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype,
+                           return_blasst_stats=return_blasst_stats)
+        o, stats = r if return_blasst_stats else (r, None)
+    else:
+        o = sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype).to(out_dtype)
+    if q_km is not None:
+        inv = q_km["inverse_order"]
+        ob = o.permute(0, 2, 1, 3).reshape(b * h, s, d)
+        o = torch.gather(ob, 1, inv.unsqueeze(-1).expand(-1, -1, d)).reshape(b, h, s, d).permute(0, 2, 1, 3).contiguous()
+    return (o, stats) if return_blasst_stats else o

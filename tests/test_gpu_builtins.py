@@ -1,0 +1,75 @@
+"""GPU unit tests of the gfx950 builtins the kernels rely on: the hardware
+FP32->E4M3 converter (v_cvt_pk_fp8_f32) and the lane layout / block scaling
+of v_mfma[_scale]_f32_32x32x64_f8f6f4."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8
+
+pytestmark = pytest.mark.gpu
+
+
+def _lib():
+    from low_bit_fake_quant import _lib as L
+    return L, L.load()
+
+
+def test_hw_cvt_matches_rne_encoder(gpu):
+    L, lib = _lib()
+    vals = np.unique(np.abs(fp8.DECODE[~np.isnan(fp8.DECODE)]).astype(np.float64))
+    mids = ((vals[:-1] + vals[1:]) / 2.0).astype(np.float32)
+    rng = np.random.default_rng(0)
+    rnd = (rng.random(200_000) * 448.0).astype(np.float32)
+    tiny = (rng.random(50_000) * 2.0 ** -5).astype(np.float32)
+    base = np.concatenate([vals.astype(np.float32), mids, np.nextafter(mids, np.float32(0)),
+                           np.nextafter(mids, np.float32(448)), rnd, tiny])
+    x = np.clip(np.concatenate([base, -base]), -448, 448).astype(np.float32)
+    if len(x) % 2:
+        x = x[:-1]
+    xt = torch.from_numpy(x).to(gpu)
+    out = torch.empty(len(x), dtype=torch.uint8, device=gpu)
+    L.check(lib.lbfq_selftest_cvt_fp8(xt.data_ptr(), len(x), out.data_ptr(), L.stream_handle()), "cvt")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = fp8.encode(x)
+    bad = np.nonzero(got != ref)[0]
+    assert len(bad) == 0, f"{len(bad)} mismatches, e.g. x={x[bad[:5]]} hw={got[bad[:5]]} ref={ref[bad[:5]]}"
+
+
+def _rand_codes(rng, shape):
+    c = rng.integers(0, 256, size=shape, dtype=np.uint8)
+    c[(c & 0x7F) == 0x7F] = 0x38  # no NaN codes
+    return c
+
+
+@pytest.mark.parametrize("scaled", [False, True])
+def test_mfma_32x32x64_layout_and_scales(gpu, scaled):
+    L, lib = _lib()
+    rng = np.random.default_rng(1 if scaled else 2)
+    A = _rand_codes(rng, (32, 64))
+    B = _rand_codes(rng, (64, 32))
+    Af = fp8.decode(A).astype(np.float64)
+    Bf = fp8.decode(B).astype(np.float64)
+    if scaled:
+        sa = rng.integers(120, 135, size=(32, 2)).astype(np.uint8)
+        sb = rng.integers(120, 135, size=(32, 2)).astype(np.uint8)
+        ref = np.zeros((32, 32))
+        for blk in range(2):
+            ks = slice(32 * blk, 32 * blk + 32)
+            fa = np.ldexp(1.0, sa[:, blk].astype(int) - 127)[:, None]
+            fb = np.ldexp(1.0, sb[:, blk].astype(int) - 127)[None, :]
+            ref += (Af[:, ks] @ Bf[ks, :]) * fa * fb
+    else:
+        ref = Af @ Bf
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    a_d, b_d = t(A), t(B)
+    sa_d = t(sa) if scaled else None
+    sb_d = t(sb) if scaled else None
+    c = torch.empty((32, 32), dtype=torch.float32, device=gpu)
+    L.check(lib.lbfq_selftest_mfma(a_d.data_ptr(), b_d.data_ptr(), L.ptr(sa_d), L.ptr(sb_d), c.data_ptr(),
+                                   L.stream_handle()), "mfma")
+    torch.cuda.synchronize()
+    got = c.cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-3 * np.abs(ref).max() * 1e-3)

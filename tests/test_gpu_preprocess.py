@@ -1,0 +1,79 @@
+"""GPU smoothing, Hadamard and k-means reorder: bit-exact vs the CPU oracle."""
+
+import pytest
+import torch
+
+from conftest import cpu_randn
+from oracle import hadamard as ohad
+from oracle import kmeans as okm
+from oracle import preprocess as opre
+
+pytestmark = pytest.mark.gpu
+
+
+def _k(shape, dtype, seed):
+    x = cpu_randn(*shape, seed=seed, dtype=torch.float32)
+    x = x + 2.0 * cpu_randn(1, 1, shape[2], shape[3], seed=seed + 1, dtype=torch.float32)
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("s", [1024, 1000])
+def test_smooth_k_bit_exact(gpu, dtype, s):
+    from low_bit_fake_quant import smooth_k
+    k = _k((2, s, 3, 128), dtype, seed=1)
+    out, mean = smooth_k(k.to(gpu))
+    ro, rm = opre.smooth_k(k)
+    assert torch.equal(mean.cpu(), rm)
+    assert torch.equal(out.cpu(), ro)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_group_mean_q_bit_exact(gpu, dtype):
+    from low_bit_fake_quant import group_mean_q
+    q = _k((1, 1024, 2, 64), dtype, seed=2)
+    out, qm = group_mean_q(q.to(gpu), block_q=256)
+    ro, rq = opre.group_mean_q(q, 256)
+    assert torch.equal(qm.cpu(), rq)
+    assert torch.equal(out.cpu(), ro)
+
+
+def test_smooth_v_bit_exact(gpu):
+    from low_bit_fake_quant import smooth_v_per_block
+    v = _k((1, 512, 2, 128), torch.bfloat16, seed=3)
+    out, alpha = smooth_v_per_block(v.to(gpu), block_s=64)
+    ro, ra = opre.smooth_v_per_block(v, 64)
+    assert torch.equal(alpha.cpu(), ra)
+    assert torch.equal(out.cpu(), ro)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("random_sign", [True, False])
+def test_hadamard_bit_exact(gpu, d, random_sign):
+    from low_bit_fake_quant import apply_qk_hadamard, hadamard_transform_last_dim
+    q = _k((1, 256, 3, d), torch.bfloat16, seed=4)
+    k = _k((1, 256, 3, d), torch.bfloat16, seed=5)
+    qr, kr = apply_qk_hadamard(q.to(gpu), k.to(gpu), random_sign=random_sign, seed=7)
+    rq, rk = ohad.apply_qk_hadamard(q, k, random_sign=random_sign, seed=7)
+    assert torch.equal(qr.cpu(), rq) and torch.equal(kr.cpu(), rk)
+    x = cpu_randn(10, 7, d, seed=9, dtype=torch.float32)
+    y = hadamard_transform_last_dim(x.to(gpu), scale=0.25)
+    assert torch.equal(y.cpu(), ohad.fwht_last_dim(x, 0.25))
+
+
+@pytest.mark.parametrize("k_clusters,iters", [(32, 10), (16, 3), (1, 2), (64, 1)])
+def test_kmeans_reorder_bit_exact(gpu, k_clusters, iters):
+    from low_bit_fake_quant import apply_kv_permutation, kmeans_reorder_tokens
+    g = torch.Generator().manual_seed(5)
+    cent = torch.randn(2, 8, 128, generator=g) * 2
+    lab = torch.randint(0, 8, (1024, 2), generator=g)
+    x = (torch.gather(cent.unsqueeze(0).expand(1024, 2, 8, 128), 2, lab.view(1024, 2, 1, 1).expand(1024, 2, 1, 128))
+         .squeeze(2) + 0.3 * torch.randn(1024, 2, 128, generator=g)).unsqueeze(0).to(torch.bfloat16)
+    r = kmeans_reorder_tokens(x.to(gpu), n_clusters=k_clusters, max_iters=iters, seed=3)
+    ref = okm.kmeans_reorder_tokens(x, n_clusters=k_clusters, max_iters=iters, seed=3)
+    assert torch.equal(r.labels.cpu(), ref["labels"])
+    assert torch.equal(r.order.cpu(), ref["order"])
+    assert torch.equal(r.inverse_order.cpu(), ref["inverse_order"])
+    assert torch.equal(r.tensor_reordered.cpu(), ref["tensor_reordered"])
+    y = cpu_randn(1, 1024, 2, 128, seed=8)
+    assert torch.equal(apply_kv_permutation(y.to(gpu), r.order).cpu(), okm.apply_kv_permutation(y, ref["order"]))

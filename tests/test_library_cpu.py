@@ -1,0 +1,125 @@
+"""CPU-side checks: the C-ABI library loads and exports every symbol
+include/lbfq.h declares; host-side guards raise the reference's errors."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import PKG_DIR, REPO
+
+
+def _declared_symbols():
+    text = open(os.path.join(REPO, "include", "lbfq.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(lbfq_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from low_bit_fake_quant import _lib
+    path = _lib.LIB_PATH
+    if not os.path.exists(path):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    syms = _declared_symbols()
+    assert len(syms) >= 10
+    for name in syms:
+        assert hasattr(lib, name), name
+    assert set(syms) == set(_lib.EXPORTED)
+
+
+def test_struct_layouts_match_header():
+    """ctypes structs mirror the C structs field by field (names, order)."""
+    from low_bit_fake_quant import _lib
+    text = open(os.path.join(REPO, "include", "lbfq.h")).read()
+    for struct, cls in (("lbfq_rowtile_params", _lib.RowTileParams), ("lbfq_attn_params", _lib.AttnParams)):
+        body = re.search(r"typedef struct \{((?:(?!typedef struct).)*?)\}\s*" + struct, text, flags=re.S).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        names = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            parts = decl.split()
+            rest = " ".join(parts[1:]) if parts[0] != "const" else " ".join(parts[2:])
+            for n in rest.split(","):
+                names.append(n.strip().lstrip("*").strip())
+        assert names == [f[0] for f in cls._fields_], struct
+
+
+def test_product_fails_loudly_without_gpu(monkeypatch):
+    from low_bit_fake_quant import _lib
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    with pytest.raises(_lib.HipLibraryError):
+        _lib.load()
+
+
+def test_reference_guard_messages_on_cpu_tensors():
+    from low_bit_fake_quant import (fake_quant_attention, fp8_block_quant, group_mean_q, kmeans_reorder_tokens,
+                                    smooth_k)
+    x = torch.zeros(1, 64, 2, 64)
+    with pytest.raises(ValueError, match="must live on CUDA"):
+        fp8_block_quant(x)
+    with pytest.raises(ValueError, match="must be 4-D NHD"):
+        fp8_block_quant(torch.zeros(64, 2, 64))
+    with pytest.raises(ValueError, match="q/k/v must live on CUDA"):
+        fake_quant_attention(x, x, x)
+    with pytest.raises(ValueError, match="shapes must match"):
+        fake_quant_attention(x, x, torch.zeros(1, 32, 2, 64))
+    with pytest.raises(ValueError, match="k must be 4-D NHD on CUDA"):
+        smooth_k(x)
+    with pytest.raises(ValueError, match="q must be 4-D NHD on CUDA"):
+        group_mean_q(x)
+    with pytest.raises(ValueError, match="t must be 4-D NHD on CUDA"):
+        kmeans_reorder_tokens(x, n_clusters=4)
+
+
+def test_kernel_config_guards():
+    from low_bit_fake_quant import QuantConfig
+    from low_bit_fake_quant.attention_kernel import parse_blasst_fill, validate_kernel_config
+
+    def v(**kw):
+        validate_kernel_config(QuantConfig(**kw), s=1024, d=128, has_qm=kw.get("smoothing", "full") == "full",
+                               has_v_alpha=kw.get("v_smooth_mode") == "per_block")
+
+    v()
+    with pytest.raises(ValueError, match="blasst_lambda must be in"):
+        v(blasst_lambda=1.5)
+    with pytest.raises(ValueError, match="unknown blasst_fill_mode"):
+        v(blasst_lambda=0.1, blasst_fill="bogus")
+    with pytest.raises(ValueError, match="blasst_fill_mode requires blasst_lambda"):
+        v(blasst_fill="mean")
+    with pytest.raises(ValueError, match=r"blasst UTA bins \(3\) must divide block_n"):
+        v(blasst_lambda=0.1, blasst_fill="uta3")
+    with pytest.raises(ValueError, match="p_mx_block_n .* currently must equal block_n"):
+        v(v_quant="mxfp8", v_mxfp8_block_size=128)
+    with pytest.raises(ValueError, match="q_smooth_block .* must be >= block_m"):
+        v(q_smooth_block_size=32)
+    with pytest.raises(ValueError, match="v_smooth_block .* must be >= block_n"):
+        v(v_smooth_mode="per_block", v_smooth_block_size=32)
+    with pytest.raises(ValueError, match="v_block_size .* must be >= block_n"):
+        v(v_quant="fp8_block", v_fp8_block_size=32)
+    with pytest.raises(ValueError, match="p_requant_block_n=64"):
+        v(p_requant_block_n=128, p_requant_block_m=128, q_smooth_block_size=256)
+    assert parse_blasst_fill("mean_a1.5", alpha=1.0, uta_bins=16) == (2, 1.5, 1)
+    assert parse_blasst_fill("uta16_a1.5", alpha=1.0, uta_bins=16) == (6, 1.5, 16)
+    assert parse_blasst_fill("uta", alpha=2.0, uta_bins=8) == (6, 2.0, 8)
+    assert parse_blasst_fill("thr_a0.25", alpha=1.0, uta_bins=16) == (5, 0.25, 1)
+
+
+def test_wan_padding_and_inputs():
+    from low_bit_fake_quant.wan import make_inputs, pad_length, pad_qkv, workloads
+    ws = workloads()
+    assert pad_length(32760, ws[1].cfg) == 32768
+    assert pad_length(32760, ws[2].cfg) == 32768
+    assert pad_length(75600, ws[4].cfg) == 75776
+    w = ws[0]
+    q, k, v = make_inputs(w, seed=0)
+    q2, _, _ = make_inputs(w, seed=0)
+    assert q.shape == (1, 1024, 2, 64) and q.dtype == torch.bfloat16 and torch.equal(q, q2)
+    qs, ks, vs = (t[:, :1000] for t in (q, k, v))
+    qp, kp, vp, n = pad_qkv(qs, ks, vs, ws[2].cfg)
+    assert n == 1000 and qp.shape[1] == 1024
+    assert torch.count_nonzero(qp[:, 1000:]) == 0
+    assert torch.equal(kp[:, 1000:], ks[:, -1:].expand(1, 24, 2, 64))
