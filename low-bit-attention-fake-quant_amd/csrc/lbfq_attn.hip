@@ -17,6 +17,14 @@
 // data movement.  Row statistics are in-lane reductions plus one exchange
 // with lane l ^ 32.
 //
+// Operand K-index layout of v_mfma[_scale]_f32_32x32x64_f8f6f4 (measured):
+// lane l supplies row/column l % 32; lane group g = l / 32 holds the 32
+// K-elements 16g + [0,16) (bytes 0..15) and 32 + 16g + [0,16) (bytes
+// 16..31); the E8M0 scale of K-block b (k in [32b, 32b+32)) comes from lane
+// (l % 32) + 32b.  MX scale blocks along D therefore align with 64-wide
+// contraction halves loaded as two 16-byte pieces, and in PV the tile's key
+// index equals the hardware K index.
+//
 // Per-query FP32 factors of the accumulator (online-softmax alpha, dynamic P
 // scale, fp8_block V scale) are folded into one rescale of O^T per tile,
 // skipped when the whole wave has factor 1 (the common qm_k case).
@@ -226,8 +234,9 @@ __global__ void __launch_bounds__(kThreadsA, 1) attn_fwd_kernel(lbfq_attn_params
     const uint8_t* qrow = a.q_codes + (bh * P + qi) * D;
 #pragma unroll
     for (int hh = 0; hh < NH; ++hh) {
-      const uint4* p = reinterpret_cast<const uint4*>(qrow + 64 * hh + 32 * g);
-      uint4 x = p[0], y = p[1];
+      // operand K-index layout: lane group g holds k = 16g+[0,16) and 32+16g+[0,16)
+      uint4 x = *reinterpret_cast<const uint4*>(qrow + 64 * hh + 16 * g);
+      uint4 y = *reinterpret_cast<const uint4*>(qrow + 64 * hh + 32 + 16 * g);
       qop[hh][0] = x.x; qop[hh][1] = x.y; qop[hh][2] = x.z; qop[hh][3] = x.w;
       qop[hh][4] = y.x; qop[hh][5] = y.y; qop[hh][6] = y.z; qop[hh][7] = y.w;
     }
@@ -325,8 +334,8 @@ __global__ void __launch_bounds__(kThreadsA, 1) attn_fwd_kernel(lbfq_attn_params
       for (int r = 0; r < 16; ++r) s[t][r] = 0.0f;
 #pragma unroll
       for (int hh = 0; hh < NH; ++hh) {
-        const uint8_t* rowp = &k_lds[cur][(32 * t + li) * KR + 64 * hh + 32 * g];
-        v8i ka = lds_read32(rowp, rowp + 16);
+        const uint8_t* rowp = &k_lds[cur][(32 * t + li) * KR + 64 * hh + 16 * g];
+        v8i ka = lds_read32(rowp, rowp + 32);
         if constexpr (QK_MX) {
           int64_t key = key0 + 32 * t + 16 * ((li >> 2) & 1) + 4 * (li >> 3) + (li & 3);
           int ke = key < S ? e8m0_of(a.k_scale[b * a.ksc_b + key * a.ksc_s + h * a.ksc_h + (2 * hh + g) * a.ksc_d])
@@ -585,7 +594,8 @@ __global__ void selftest_mfma_kernel(const uint8_t* A, const uint8_t* Bm, const 
   for (int q = 0; q < 8; ++q) {
     int wa = 0, wb = 0;
     for (int k = 0; k < 4; ++k) {
-      int kk = 32 * g + 4 * q + k;
+      int slot = 4 * q + k;
+      int kk = slot < 16 ? 16 * g + slot : 32 + 16 * g + (slot - 16);
       wa |= static_cast<int>(A[li * 64 + kk]) << (8 * k);
       wb |= static_cast<int>(Bm[kk * 32 + li]) << (8 * k);
     }

@@ -354,9 +354,11 @@ def _dequant_v(fp8, scale, meta, dtype):
     raise ValueError(f"bad meta: {meta!r}")
 
 
-def _attention_fp32(qb, kb, vb, sm_scale, *, corr_q=None, corr_k=None, group=None, chunk=512):
+def _attention_fp32(qb, kb, vb, sm_scale, *, corr_q=None, corr_k=None, group=None, chunk=512, p_dtype=None):
     """softmax(q k^T * scale [+ corr]) v over BHSD tensors in fp32 with contiguous
-    operands, chunked over queries (bounded memory)."""
+    operands, chunked over queries (bounded memory).  ``p_dtype`` rounds the
+    probabilities before the PV product (the reference's chunked path casts P to
+    the SDPA dtype, attention.py:318-319)."""
     B, H, S, D = qb.shape
     kT = kb.float().transpose(-2, -1).contiguous()
     vf = vb.float().contiguous()
@@ -369,6 +371,8 @@ def _attention_fp32(qb, kb, vb, sm_scale, *, corr_q=None, corr_k=None, group=Non
         if corr_q is not None:
             scores = scores + torch.matmul(corr_q[:, :, grp_idx[m0:m1]].float().contiguous(), ksT) * sm_scale
         p = torch.softmax(scores, dim=-1)
+        if p_dtype is not None:
+            p = p.to(p_dtype).float()
         out[:, :, m0:m1] = torch.matmul(p, vf)
     return out
 
@@ -393,7 +397,7 @@ def _fake_quant_attention_sdpa(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scal
         o = _attention_fp32(qb, kb, vb, sm_scale).to(sdpa_dtype)
     else:
         o = _attention_fp32(qb, kb, vb, sm_scale, corr_q=qm.permute(*perm), corr_k=k_work.permute(*perm),
-                            group=cfg.q_smooth_block_size).to(sdpa_dtype)
+                            group=cfg.q_smooth_block_size, p_dtype=sdpa_dtype).to(sdpa_dtype)
     return o.permute(*perm).contiguous()
 
 

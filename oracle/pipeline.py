@@ -104,13 +104,16 @@ def qk_quant_inputs(q_work, k_work, cfg):
 
 
 def p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype, rows=None,
-                   return_blasst_stats=False):
+                   return_blasst_stats=False, qk_dequant_dtype=torch.bfloat16):
+    """``qk_dequant_dtype=torch.bfloat16`` is the reference (attention.py:534-535);
+    ``torch.float32`` keeps the dequantised Q/K exact and is used only to measure
+    how sensitive the reference output is to that rounding."""
     b, s, h, d = q_work.shape
     qi, ki = qk_quant_inputs(q_work, k_work, cfg)
     qc, qs, qmeta = quant_qk(qi, cfg)
     kc, ks, kmeta = quant_qk(ki, cfg)
-    q_deq = dequant_qk(qc, qs, qmeta, torch.bfloat16)
-    k_deq = dequant_qk(kc, ks, kmeta, torch.bfloat16)
+    q_deq = dequant_qk(qc, qs, qmeta, qk_dequant_dtype)
+    k_deq = dequant_qk(kc, ks, kmeta, qk_dequant_dtype)
     vc, vs, vmeta = quant_v(v_work, cfg)
     v_block_scale, v_block_size = None, 0
     if vmeta[0] == "fp8_channel":
@@ -185,7 +188,8 @@ def sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype):
     return torch.matmul(p, vb).to(sdpa_dtype).permute(*perm).contiguous()
 
 
-def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=False):
+def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=False,
+                         qk_dequant_dtype=torch.bfloat16):
     if q.shape != k.shape or q.shape != v.shape:
         raise ValueError("q/k/v shapes must match")
     out_dtype = q.dtype
@@ -199,7 +203,7 @@ def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=Fal
     stats = None
     if cfg.p_requant:
         r = p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype,
-                           return_blasst_stats=return_blasst_stats)
+                           return_blasst_stats=return_blasst_stats, qk_dequant_dtype=qk_dequant_dtype)
         o, stats = r if return_blasst_stats else (r, None)
     else:
         o = sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype).to(out_dtype)
