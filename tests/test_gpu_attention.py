@@ -4,7 +4,8 @@ Tolerance written here (north star: cosine >= 0.9999, max |diff| <= 1e-2):
 
 * cosine >= 0.9999 against the oracle's fake-quant output (the reference
   algorithm, not SDPA) on identical inputs;
-* at most 1% of the outputs differ by more than 1e-2;
+* the fraction of outputs differing by more than 1e-2 is at most
+  max(1%, 2 x the reference's own fraction, see below);
 * max |diff| <= 1e-2 + max(delta_ref, max|V| / 16).
 
 Why the last two: P is requantised to E4M3 (3 mantissa bits), so a score that
@@ -13,9 +14,10 @@ p).  The FP8 kernel never rounds the dequantised Q/K to bf16 (the reference
 does, attention.py:534-535) and the gfx950 FP8 MFMA accumulates with ~1e-4
 relative precision, so a few scores land on the other side of a boundary.
 One flipped code of a dominant probability moves that output by up to half
-an E4M3 step of |V| (max|V| / 16).  delta_ref is the reference's own
-sensitivity, measured on the same inputs: the max |diff| between the
-reference as written and the reference with exact fp32 dequantised Q/K.
+an E4M3 step of |V| (max|V| / 16); outputs of magnitude 2..4 also have a
+bf16 ulp of 1/64 > 1e-2.  delta_ref and the reference's own fraction are its
+self-sensitivity, measured on the same inputs: the reference as written vs
+the same reference with exact fp32 dequantised Q/K.
 Codes, scales and permutations are checked bit-exactly in the other GPU
 tests.
 """
@@ -45,9 +47,10 @@ def check_parity(out, q, k, v, cfg, label=""):
     half_step = v.float().abs().max().item() / 16.0
     c, m = cosine(out, ref), max_abs(out, ref)
     frac = ((out.float() - ref.float()).abs() > MAXABS).float().mean().item()
+    frac_ref = ((ref32.float() - ref.float()).abs() > MAXABS).float().mean().item()
     assert torch.isfinite(out).all()
-    assert c >= cos_min and frac <= 0.01 and m <= MAXABS + max(delta_ref, half_step), (
-        f"{label}: cos={c:.6f} maxabs={m:.3e} delta_ref={delta_ref:.3e} frac>1e-2={frac:.2e}")
+    assert c >= cos_min and frac <= max(0.01, 2 * frac_ref) and m <= MAXABS + max(delta_ref, half_step), (
+        f"{label}: cos={c:.6f} maxabs={m:.3e} delta_ref={delta_ref:.3e} frac>1e-2={frac:.2e} ref={frac_ref:.2e}")
     return c, m, delta_ref, frac
 
 
