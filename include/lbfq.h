@@ -72,6 +72,7 @@ typedef struct {
   uint32_t* amax_table;                    /* (B,H,D) fp32 bits, channel modes  */
   int mx_block;                            /* MX-QK columns per scale (8..D)    */
   int smoothed_stage;                      /* 0: after subtract, 1: after FWHT  */
+  int scale_e8m0;                          /* MX modes: write E8M0 bytes, not fp32 */
 } lbfq_rowtile_params;
 
 int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream);
@@ -110,12 +111,13 @@ int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64
 /* ---- qm_k row-max estimate + qm correction table --------------------------
  * Replaces attention.py:366-395 (_estimate_rowmax_from_qm_k) and precomputes
  * the kernel's qm correction attention_triton.py:156-160:
- *   bias[b,h,g,n]   = (qm[b,g,h,:] . K_s[b,n,h,:]) * sm_scale   (fp32)
+ *   bias[b,h,g,n]   = (qm[b,g,h,:] . K_s[b,n,h,:]) * scale       (fp32)
  *   rowmax[b,h,g]   = max_n bias[b,h,g,n]
+ * (the attention path passes scale = sm_scale * log2(e): scores in log2 units)
  * K_s is NHD (dtype) optionally gathered by `gather` (V-kmeans order).
  * bias is (B,H,G,s_pitch) (NULL to skip), rowmax (B,H,G) (NULL to skip). */
 int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, int64_t B, int64_t S,
-             int64_t H, int64_t D, int64_t G, float sm_scale, float* bias, int64_t s_pitch, float* rowmax,
+             int64_t H, int64_t D, int64_t G, float scale, float* bias, int64_t s_pitch, float* rowmax,
              lbfq_stream_t stream);
 
 /* ---- FP8-MFMA P-requant attention ------------------------------------------
@@ -128,25 +130,24 @@ typedef struct {
   const uint8_t* q_codes;         /* (B,H,s_pitch,D)                               */
   const uint8_t* k_codes;         /* (B,H,s_pitch,D)                               */
   const uint8_t* v_codes_t;       /* (B,H,D,s_pitch)                               */
-  int qk_mx;                      /* 0: fp8_block scales, 1: MX (block 32 along D) */
-  const float* q_scale;           /* fp8_block: [b*sb + (s/qk_block)*ss + h*sh]    */
-  const float* k_scale;           /* mx: [b*sb + s*ss + h*sh + (d/32)*sd]          */
-  int64_t qsc_b, qsc_s, qsc_h, qsc_d;
-  int64_t ksc_b, ksc_s, ksc_h, ksc_d;
-  int qk_block;                   /* fp8_block rows per scale (multiple of 16)     */
-  int v_kind;                     /* 0 channel (B,H,D), 1 block (B,S/vb,H), 2 mx (B,S/vb,H,D) */
-  const float* v_scale;
-  int v_block;                    /* rows per V scale (kinds 1, 2; multiple of 64) */
+  int qk_mx;                      /* 0: fp8_block scales, 1: MX E8M0 per 32 along D */
+  const void* q_scale;            /* fp8_block: (B,H,S/qk_block) fp32;             */
+  const void* k_scale;            /* mx: (B,H,s_pitch,D/32) E8M0 bytes             */
+  int qk_block;                   /* fp8_block rows per scale: power of two >= 16  */
+  int v_kind;                     /* 0 channel, 1 fp8_block, 2 mx                  */
+  const void* v_scale;            /* channel (B,H,D) fp32; block (B,H,S/vb) fp32;  */
+                                  /* mx (B,H,S/vb,D) E8M0 bytes                    */
+  int v_block;                    /* rows per V scale: power of two, >= 64         */
   int p_mode;                     /* 0 elementwise, 1 mx, 2 dynamic               */
   float sm_scale;
   int p_max_offset;
-  int block_m;                    /* BLASST stats granularity (multiple of 32)     */
-  const float* qk_bias;           /* (B,H,G,s_pitch) natural units, or NULL        */
-  int q_group;                    /* rows per qm group (multiple of 32)            */
-  const float* rowmax_est;        /* per-group (B,H,G) natural units, or NULL       */
+  int block_m;                    /* BLASST stats rows per block (> 0)             */
+  const float* qk_bias;           /* (B,H,G,s_pitch) qm.K_s*sm_scale*log2(e), or NULL */
+  int q_group;                    /* rows per qm group: power of two >= 32         */
+  const float* rowmax_est;        /* (B,H,G) estimate in log2 units, or NULL       */
   int rowmax_dynamic;             /* 1: qm_k thresholds (dynamic P), 0: fixed m    */
-  const float* v_alpha;           /* (B,S/vsb,H,D) fp32 or NULL                    */
-  int v_smooth_block;             /* multiple of 64                                */
+  const float* v_alpha;           /* (B,H,S/vsb,D) fp32 or NULL                    */
+  int v_smooth_block;             /* power of two, >= 64                           */
   float blasst_lambda;            /* <= 0 disables BLASST                          */
   int blasst_fill;                /* 0 zero,1 max,2 mean,3 logn,4 sample8,5 thr,6 uta */
   float blasst_fill_alpha;

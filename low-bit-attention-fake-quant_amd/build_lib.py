@@ -33,6 +33,9 @@ UNITS = {
     "lbfq_kmeans.hip": ["-ffp-contract=off"],
     "lbfq_qmk.hip": ["-ffp-contract=off"],
     "lbfq_attn.hip": [],
+    "lbfq_attn_p0.hip": [],
+    "lbfq_attn_p1.hip": [],
+    "lbfq_attn_p2.hip": [],
 }
 
 

@@ -1,0 +1,9 @@
+// Instantiations of the attention kernel for P quant mode 0 (0 elementwise,
+// 1 mx, 2 dynamic); split per mode so the translation units build in parallel.
+#include "lbfq_attn_kernel.h"
+
+namespace lbfq_attn {
+int launch_p0(const KArgs& a, int D, bool qk_mx, int rb, bool blasst, bool valpha, hipStream_t st) {
+  return launch_p<0>(a, D, qk_mx, rb, blasst, valpha, st);
+}
+}  // namespace lbfq_attn

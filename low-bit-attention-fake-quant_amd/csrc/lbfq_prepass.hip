@@ -56,6 +56,7 @@ struct RowTileArgs {
   uint32_t* amax_table;
   int mx_block;
   int smoothed_stage;
+  int scale_e8m0;
 };
 
 __device__ __forceinline__ void load8(const void* x, int dt, int64_t idx, float v[8]) {
@@ -230,7 +231,9 @@ __global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
           m = fmaxf(m, kAmaxFloor);
           float sc = mx_scale_from_amax(m);
           sc_sh[threadIdx.x] = sc;
-          a.scale[b * a.sc_b + tile * a.sc_s + h * a.sc_h + threadIdx.x * a.sc_d] = sc;
+          int64_t si = b * a.sc_b + tile * a.sc_s + h * a.sc_h + threadIdx.x * a.sc_d;
+          if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
+          else a.scale[si] = sc;
         }
       }
       __syncthreads();
@@ -270,8 +273,11 @@ __global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
       float sc = mx_scale_from_amax(m);
 #pragma unroll
       for (int i = 0; i < 8; ++i) sc8[i] = sc;
-      if (valid && (lane & (ml - 1)) == 0)
-        a.scale[b * a.sc_b + s * a.sc_s + h * a.sc_h + (d0 / a.mx_block) * a.sc_d] = sc;
+      if (valid && (lane & (ml - 1)) == 0) {
+        int64_t si = b * a.sc_b + s * a.sc_s + h * a.sc_h + (d0 / a.mx_block) * a.sc_d;
+        if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
+        else a.scale[si] = sc;
+      }
     }
     uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -396,6 +402,7 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   a.amax_table = p->amax_table;
   a.mx_block = p->mx_block;
   a.smoothed_stage = p->smoothed_stage;
+  a.scale_e8m0 = p->scale_e8m0;
   int64_t ntile = (p->S + p->R - 1) / p->R;
   int64_t nblocks = p->B * p->H * ntile;
   LBFQ_CHECK_ARG(nblocks < (1ll << 31), "lbfq_rowtile: grid too large");

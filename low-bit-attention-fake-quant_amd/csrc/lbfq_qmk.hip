@@ -1,7 +1,8 @@
 // qm . K_smooth products for Q smoothing (gfx950).
 //
-//   bias[b,h,g,n] = (qm[b,g,h,:] . K_s[b,n,h,:]) * sm_scale      (fp32)
+//   bias[b,h,g,n] = (qm[b,g,h,:] . K_s[b,n,h,:]) * scale         (fp32)
 //   rowmax[b,h,g] = max_n bias[b,h,g,n]
+// The attention path uses scale = sm_scale * log2(e) (scores in log2 units).
 //
 // bias is the per-key correction the reference adds to every score inside the
 // attention K-loop (attention_triton.py:156-160); rowmax is the qm_k row-max
@@ -28,7 +29,7 @@ __device__ __forceinline__ float from_ordered_bits(uint32_t u) {
 
 template <int D>
 __global__ void __launch_bounds__(256) qmk_kernel(const float* qm, const void* ks, int dt, const int32_t* gather,
-                                                  int64_t B, int64_t S, int64_t H, int64_t G, float sm_scale,
+                                                  int64_t B, int64_t S, int64_t H, int64_t G, float scale,
                                                   float* bias, int64_t s_pitch, uint32_t* rowmax_bits) {
   __shared__ float q_lds[kGChunk * D];
   __shared__ float k_lds[kKeys * (D + 1)];
@@ -63,7 +64,7 @@ __global__ void __launch_bounds__(256) qmk_kernel(const float* qm, const void* k
       float acc = 0.0f;
 #pragma unroll 16
       for (int d = 0; d < D; ++d) acc = fmaf(q_lds[gg * D + d], k_lds[j * (D + 1) + d], acc);
-      float v = acc * sm_scale;
+      float v = acc * scale;
       if (n < S) {
         if (bias) bias[(bh * G + g0 + gg) * s_pitch + n] = v;
       }
@@ -89,7 +90,7 @@ __global__ void decode_ordered_kernel(uint32_t* p, int64_t n) {
 }  // namespace
 
 extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, int64_t B, int64_t S,
-                        int64_t H, int64_t D, int64_t G, float sm_scale, float* bias, int64_t s_pitch, float* rowmax,
+                        int64_t H, int64_t D, int64_t G, float scale, float* bias, int64_t s_pitch, float* rowmax,
                         lbfq_stream_t stream) {
   LBFQ_CHECK_ARG(qm && ks && (bias || rowmax), "lbfq_qmk: null pointer");
   LBFQ_CHECK_ARG(D == 64 || D == 128, "lbfq_qmk: D must be 64 or 128");
@@ -104,10 +105,10 @@ extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int
   const int64_t nblk = B * H * ((S + kKeys - 1) / kKeys);
   if (D == 128)
     hipLaunchKernelGGL(qmk_kernel<128>, dim3(static_cast<unsigned>(nblk)), dim3(256), 0, st, qm, ks, ks_dtype, gather,
-                       B, S, H, G, sm_scale, bias, s_pitch, rb);
+                       B, S, H, G, scale, bias, s_pitch, rb);
   else
     hipLaunchKernelGGL(qmk_kernel<64>, dim3(static_cast<unsigned>(nblk)), dim3(256), 0, st, qm, ks, ks_dtype, gather,
-                       B, S, H, G, sm_scale, bias, s_pitch, rb);
+                       B, S, H, G, scale, bias, s_pitch, rb);
   LBFQ_LAUNCH_CHECK("lbfq_qmk");
   if (rb) {
     hipLaunchKernelGGL(decode_ordered_kernel, dim3(static_cast<unsigned>((nr + 255) / 256)), dim3(256), 0, st, rb, nr);

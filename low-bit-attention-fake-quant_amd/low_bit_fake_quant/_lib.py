@@ -48,6 +48,7 @@ class RowTileParams(ctypes.Structure):
         ("amax_table", _vp),
         ("mx_block", _i32),
         ("smoothed_stage", _i32),
+        ("scale_e8m0", _i32),
     ]
 
 
@@ -57,12 +58,10 @@ class AttnParams(ctypes.Structure):
         ("s_pitch", _i64),
         ("q_codes", _vp), ("k_codes", _vp), ("v_codes_t", _vp),
         ("qk_mx", _i32),
-        ("q_scale", _vp), ("k_scale", _vp),
-        ("qsc_b", _i64), ("qsc_s", _i64), ("qsc_h", _i64), ("qsc_d", _i64),
-        ("ksc_b", _i64), ("ksc_s", _i64), ("ksc_h", _i64), ("ksc_d", _i64),
+        ("q_scale", _vp),
+        ("k_scale", _vp),
         ("qk_block", _i32),
-        ("v_kind", _i32),
-        ("v_scale", _vp),
+        ("v_kind", _i32), ("v_scale", _vp),
         ("v_block", _i32),
         ("p_mode", _i32),
         ("sm_scale", _f32),

@@ -43,7 +43,7 @@ def rowtile(src: RowSource, *, R: int, smoothed: torch.Tensor | None = None, smo
             signs: torch.Tensor | None = None, hadamard: bool = False, had_scale: float = 1.0,
             quant_mode: int = _lib.Q_NONE, codes: torch.Tensor | None = None, codes_layout: int = _lib.LAYOUT_NHD,
             codes_spitch: int = 0, scale: torch.Tensor | None = None, scale_strides=(0, 0, 0, 0),
-            amax_table: torch.Tensor | None = None, mx_block: int = 32) -> None:
+            amax_table: torch.Tensor | None = None, mx_block: int = 32, scale_e8m0: bool = False) -> None:
     lib = _lib.load()
     x = src.x
     b, s, h, d = x.shape
@@ -62,6 +62,7 @@ def rowtile(src: RowSource, *, R: int, smoothed: torch.Tensor | None = None, smo
     p.amax_table = _lib.ptr(amax_table)
     p.mx_block = int(mx_block)
     p.smoothed_stage = int(smoothed_stage)
+    p.scale_e8m0 = 1 if scale_e8m0 else 0
     _lib.check(lib.lbfq_rowtile(p, _lib.stream_handle(x.device)), "lbfq_rowtile")
 
 

@@ -36,6 +36,8 @@ from .attention_kernel import launch_attention, parse_blasst_fill, validate_kern
 from .config import QuantConfig
 from .hadamard import apply_qk_hadamard, qk_signs_device
 from .kmeans import KMeansReorderResult, gather_rows, kmeans_labels, make_result
+LOG2E = 1.4426950408889634
+
 from .quant import (
     fp8_block_dequant,
     fp8_block_quant,
@@ -186,7 +188,8 @@ def _kmeans_result(src_tensor, km) -> Optional[KMeansReorderResult]:
 
 
 def _quant_qk_codes(src: RowSource, cfg: QuantConfig, P: int, *, signs, k_smooth_out=None):
-    """Quantise one of Q/K into head-major codes (B,H,P,D); returns (codes, scale, strides)."""
+    """Quantise one of Q/K into head-major codes (B,H,P,D) and the kernel's scales:
+    fp8_block -> (B,H,S/block) fp32; mxfp8 -> (B,H,P,D/32) E8M0 bytes."""
     b, s, h, d = src.shape
     dev = src.x.device
     codes = (torch.zeros if P > s else torch.empty)((b, h, P, d), dtype=torch.uint8, device=dev)
@@ -195,27 +198,30 @@ def _quant_qk_codes(src: RowSource, cfg: QuantConfig, P: int, *, signs, k_smooth
         blk = cfg.fp8_block_size
         if s % blk != 0:
             raise ValueError(f"S={s} must be divisible by block_s={blk}")
-        scale = torch.empty((b, s // blk, h), dtype=torch.float32, device=dev)
-        strides = (scale.stride(0), scale.stride(1), scale.stride(2), 0)
+        nb = s // blk
+        scale = torch.empty((b, h, nb), dtype=torch.float32, device=dev)
         rowtile(src, R=blk, hadamard=cfg.qk_hadamard, signs=signs, had_scale=hs, quant_mode=_lib.Q_FP8_BLOCK,
-                codes=codes, codes_layout=_lib.LAYOUT_BHSD, codes_spitch=P, scale=scale, scale_strides=strides,
-                smoothed=k_smooth_out)
+                codes=codes, codes_layout=_lib.LAYOUT_BHSD, codes_spitch=P, scale=scale,
+                scale_strides=(h * nb, 1, nb, 0), smoothed=k_smooth_out)
     elif cfg.qk_quant == "mxfp8":
         bd = cfg.mxfp8_block_size
         if d % bd != 0:
             raise ValueError(f"D={d} must be divisible by block_d={bd}")
-        scale = torch.empty((b, s, h, d // bd), dtype=torch.float32, device=dev)
-        strides = scale.stride()
+        nb = d // bd
+        # padding rows keep E8M0 0 (2^-127): finite, and their codes are zero
+        scale = torch.zeros((b, h, P, nb), dtype=torch.uint8, device=dev)
         rowtile(src, R=64, hadamard=cfg.qk_hadamard, signs=signs, had_scale=hs, quant_mode=_lib.Q_MX_QK,
-                codes=codes, codes_layout=_lib.LAYOUT_BHSD, codes_spitch=P, scale=scale, scale_strides=strides,
-                mx_block=bd, smoothed=k_smooth_out)
+                codes=codes, codes_layout=_lib.LAYOUT_BHSD, codes_spitch=P, scale=scale,
+                scale_strides=(h * P * nb, nb, P * nb, 1), mx_block=bd, smoothed=k_smooth_out, scale_e8m0=True)
     else:
         raise ValueError(f"unsupported qk_quant: {cfg.qk_quant!r}")
-    return codes, scale, strides
+    return codes, scale
 
 
 def _quant_v_codes(src: RowSource, cfg: QuantConfig, P: int):
-    """Quantise V into transposed codes (B,H,D,P); returns (codes_t, scale, v_kind, v_block)."""
+    """Quantise V into transposed codes (B,H,D,P) and the kernel's scales:
+    channel (B,H,D) fp32, fp8_block (B,H,S/vb) fp32, mxfp8 (B,H,S/vb,D) E8M0.
+    Returns (codes_t, scale, v_kind, v_block)."""
     b, s, h, d = src.shape
     dev = src.x.device
     codes = (torch.zeros if P > s else torch.empty)((b, h, d, P), dtype=torch.uint8, device=dev)
@@ -229,44 +235,45 @@ def _quant_v_codes(src: RowSource, cfg: QuantConfig, P: int):
         vb = cfg.v_fp8_block_size
         if s % vb != 0:
             raise ValueError(f"S={s} must be divisible by block_s={vb}")
-        scale = torch.empty((b, s // vb, h), dtype=torch.float32, device=dev)
+        nb = s // vb
+        scale = torch.empty((b, h, nb), dtype=torch.float32, device=dev)
         rowtile(src, R=vb, quant_mode=_lib.Q_FP8_BLOCK, codes=codes, codes_layout=_lib.LAYOUT_BHDS, codes_spitch=P,
-                scale=scale, scale_strides=(scale.stride(0), scale.stride(1), scale.stride(2), 0))
+                scale=scale, scale_strides=(h * nb, 1, nb, 0))
         return codes, scale, 1, vb
     if cfg.v_quant == "mxfp8":
         vb = cfg.v_mxfp8_block_size
         if s % vb != 0:
             raise ValueError(f"S={s} must be divisible by block_s={vb}")
-        scale = torch.empty((b, s // vb, h, d), dtype=torch.float32, device=dev)
+        nb = s // vb
+        scale = torch.empty((b, h, nb, d), dtype=torch.uint8, device=dev)
         rowtile(src, R=vb, quant_mode=_lib.Q_MX_V, codes=codes, codes_layout=_lib.LAYOUT_BHDS, codes_spitch=P,
-                scale=scale, scale_strides=scale.stride())
+                scale=scale, scale_strides=(h * nb * d, d, nb * d, 1), scale_e8m0=True)
         return codes, scale, 2, vb
     raise ValueError(f"unsupported v_quant: {cfg.v_quant!r}")
 
 
 @dataclass
 class QuantizedOperands:
-    """Everything the attention kernel reads, in its HBM layouts."""
+    """Everything the attention kernel reads, in its HBM layouts (head-major,
+    S padded to the pitch P with zero codes)."""
 
     b: int
     s: int
     h: int
     d: int
     P: int
-    q_codes: torch.Tensor
-    q_scale: torch.Tensor
-    q_strides: tuple
-    k_codes: torch.Tensor
+    q_codes: torch.Tensor                 # (B,H,P,D) E4M3
+    q_scale: torch.Tensor                 # fp8_block (B,H,S/blk) fp32 | mx (B,H,P,D/32) E8M0
+    k_codes: torch.Tensor                 # (B,H,P,D) E4M3
     k_scale: torch.Tensor
-    k_strides: tuple
-    v_codes_t: torch.Tensor
-    v_scale: torch.Tensor
+    v_codes_t: torch.Tensor               # (B,H,D,P) E4M3
+    v_scale: torch.Tensor                 # channel (B,H,D) | block (B,H,S/vb) | mx (B,H,S/vb,D) E8M0
     v_kind: int
     v_block: int
-    bias: Optional[torch.Tensor]
-    rowmax: Optional[torch.Tensor]
-    v_alpha: Optional[torch.Tensor]
-    out_row_map: Optional[torch.Tensor]
+    bias: Optional[torch.Tensor]          # (B,H,G,P) qm.K_s * sm_scale * log2(e)
+    rowmax: Optional[torch.Tensor]        # (B,H,G) max_n bias (log2 units)
+    v_alpha: Optional[torch.Tensor]       # (B,H,S/vsb,D) fp32
+    out_row_map: Optional[torch.Tensor]   # (B*H,S) int32
 
 
 def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> QuantizedOperands:
@@ -278,9 +285,9 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
     signs = None
     if cfg.qk_hadamard and cfg.qk_hadamard_random_sign:
         signs = qk_signs_device(h, d, cfg.qk_hadamard_seed, prep.q.x.device)
-    q_codes, q_scale, q_str = _quant_qk_codes(prep.q, cfg, P, signs=signs)
+    q_codes, q_scale = _quant_qk_codes(prep.q, cfg, P, signs=signs)
     k_s = torch.empty_like(prep.k.x) if has_qm else None
-    k_codes, k_scale, k_str = _quant_qk_codes(prep.k, cfg, P, signs=signs, k_smooth_out=k_s)
+    k_codes, k_scale = _quant_qk_codes(prep.k, cfg, P, signs=signs, k_smooth_out=k_s)
     v_codes, v_scale, v_kind, v_block = _quant_v_codes(prep.v, cfg, P)
     bias = rowmax = None
     if cfg.rowmax_mode == "qm_k":
@@ -289,11 +296,14 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
     elif cfg.rowmax_mode != "online":
         raise ValueError(f"unsupported rowmax_mode: {cfg.rowmax_mode!r}")
     if has_qm:
-        bias, rowmax = qmk(prep.qm, k_s, sm_scale, s_pitch=P, want_rowmax=cfg.rowmax_mode == "qm_k")
-    return QuantizedOperands(b=b, s=s, h=h, d=d, P=P, q_codes=q_codes, q_scale=q_scale, q_strides=q_str,
-                             k_codes=k_codes, k_scale=k_scale, k_strides=k_str, v_codes_t=v_codes, v_scale=v_scale,
-                             v_kind=v_kind, v_block=v_block, bias=bias, rowmax=rowmax, v_alpha=prep.v_alpha,
-                             out_row_map=prep.q_order_i32())
+        # scores are handled in log2 units by the kernel
+        bias, rowmax = qmk(prep.qm, k_s, sm_scale * LOG2E, s_pitch=P, want_rowmax=cfg.rowmax_mode == "qm_k")
+    v_alpha = None
+    if prep.v_alpha is not None:
+        v_alpha = prep.v_alpha.permute(0, 2, 1, 3).contiguous()
+    return QuantizedOperands(b=b, s=s, h=h, d=d, P=P, q_codes=q_codes, q_scale=q_scale, k_codes=k_codes,
+                             k_scale=k_scale, v_codes_t=v_codes, v_scale=v_scale, v_kind=v_kind, v_block=v_block,
+                             bias=bias, rowmax=rowmax, v_alpha=v_alpha, out_row_map=prep.q_order_i32())
 
 
 def _p_requant_hip(prep: _Prep, cfg: QuantConfig, sm_scale: float, out_dtype: torch.dtype,

@@ -118,20 +118,31 @@ def validate_kernel_config(cfg, *, s: int, d: int, has_qm: bool, has_v_alpha: bo
     elif cfg.blasst_fill not in ("zero", None):
         raise ValueError("blasst_fill_mode requires blasst_lambda")
     # ---- limits of the gfx950 kernel -------------------------------------
+    def pow2(x):
+        return x > 0 and (x & (x - 1)) == 0
+
     if block_n != KERNEL_BLOCK_N:
         raise ValueError(f"the gfx950 P-requant kernel runs p_requant_block_n={KERNEL_BLOCK_N}; got {block_n}")
-    if block_m % 32 != 0:
-        raise ValueError(f"the gfx950 P-requant kernel needs p_requant_block_m to be a multiple of 32; got {block_m}")
+    if block_m <= 0:
+        raise ValueError(f"p_requant_block_m must be > 0; got {block_m}")
     if cfg.qk_quant == "mxfp8" and cfg.mxfp8_block_size != 32:
         raise ValueError("the gfx950 MX attention consumes E8M0 scales per 32 elements along D; "
                          f"mxfp8_block_size must be 32, got {cfg.mxfp8_block_size}")
-    if cfg.qk_quant == "fp8_block" and cfg.fp8_block_size % 16 != 0:
-        raise ValueError(f"fp8_block_size must be a multiple of 16 for the gfx950 kernel; got {cfg.fp8_block_size}")
-    if cfg.v_quant == "mxfp8" and cfg.v_mxfp8_block_size % KERNEL_BLOCK_N != 0:
-        raise ValueError(f"v_mxfp8_block_size must be a multiple of {KERNEL_BLOCK_N} for the gfx950 kernel; "
+    if cfg.qk_quant == "fp8_block" and not (pow2(cfg.fp8_block_size) and cfg.fp8_block_size >= 16):
+        raise ValueError(f"fp8_block_size must be a power of two >= 16 for the gfx950 kernel; got {cfg.fp8_block_size}")
+    if cfg.v_quant == "mxfp8" and not (pow2(cfg.v_mxfp8_block_size) and cfg.v_mxfp8_block_size >= KERNEL_BLOCK_N):
+        raise ValueError(f"v_mxfp8_block_size must be a power of two >= {KERNEL_BLOCK_N} for the gfx950 kernel; "
                          f"got {cfg.v_mxfp8_block_size}")
+    if cfg.v_quant == "fp8_block" and not pow2(cfg.v_fp8_block_size):
+        raise ValueError(f"v_fp8_block_size must be a power of two for the gfx950 kernel; got {cfg.v_fp8_block_size}")
     if cfg.v_quant == "fp8_block" and cfg.v_fp8_block_size > 512:
         raise ValueError("v_fp8_block_size above 512 is not supported by the gfx950 V quantiser")
+    if has_v_alpha and not pow2(cfg.v_smooth_block_size):
+        raise ValueError(f"v_smooth_block_size must be a power of two for the gfx950 kernel; "
+                         f"got {cfg.v_smooth_block_size}")
+    if has_qm and not (pow2(cfg.q_smooth_block_size) and cfg.q_smooth_block_size >= 32):
+        raise ValueError(f"q_smooth_block_size must be a power of two >= 32 for the gfx950 kernel; "
+                         f"got {cfg.q_smooth_block_size}")
 
 
 def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, return_blasst_stats: bool = False):
@@ -145,8 +156,6 @@ def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, retur
     p.q_codes, p.k_codes, p.v_codes_t = ops.q_codes.data_ptr(), ops.k_codes.data_ptr(), ops.v_codes_t.data_ptr()
     p.qk_mx = 1 if cfg.qk_quant == "mxfp8" else 0
     p.q_scale, p.k_scale = ops.q_scale.data_ptr(), ops.k_scale.data_ptr()
-    p.qsc_b, p.qsc_s, p.qsc_h, p.qsc_d = ops.q_strides
-    p.ksc_b, p.ksc_s, p.ksc_h, p.ksc_d = ops.k_strides
     p.qk_block = cfg.fp8_block_size if cfg.qk_quant == "fp8_block" else 0
     p.v_kind = ops.v_kind
     p.v_scale = ops.v_scale.data_ptr()
