@@ -54,7 +54,6 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kQB = kWaves * 32;  // queries per workgroup
 constexpr int kTN = 64;           // keys per tile (== reference block_n)
-constexpr int kVR = kTN + 16;     // LDS row pitch of V^T (bytes)
 
 enum { RB_ONLINE = 0, RB_ONLINE_BIAS = 1, RB_EST_BIAS = 2 };
 enum { FILL_ZERO = 0, FILL_MAX, FILL_MEAN, FILL_LOGN, FILL_SAMPLE8, FILL_THR, FILL_UTA };
@@ -85,13 +84,17 @@ struct KArgs {
   const int32_t* out_row_map;
 };
 
-template <int D>
-struct TileMeta {
+// Per-tile metadata staged in LDS next to the K / V^T codes.  The K side is
+// consumed by the softmax of the tile, the V side by its PV product.
+struct KMeta {
   float bias[kWaves][kTN];  // qm correction (log2 units) of each wave's group
   float ksc[4];             // fp8_block K scale of each 16-key group
-  uint32_t ke[kTN];         // MX: E8M0 bytes of the key's D/32 chunks
+};
+
+template <int D>
+struct VMeta {
+  uint32_t ve[D / 4];       // E8M0 byte of each V column (4 per word); 127 unless V is MX
   float vsc;                // fp8_block V scale of the tile
-  uint32_t ve[D / 4];       // MX: E8M0 byte of each V column (4 per word)
   float valpha[D];          // V block mean of the tile
 };
 
@@ -111,6 +114,35 @@ __device__ __forceinline__ v8i lds_read32(const uint8_t* p0, const uint8_t* p1) 
   r[4] = y.x; r[5] = y.y; r[6] = y.z; r[7] = y.w;
   return r;
 }
+
+// Asynchronous global -> LDS copies (gfx950 global_load_lds): every active
+// lane copies 16 (or 4) bytes from its own global address to
+// lds_base + lane * 16 (or 4); lds_base is wave-uniform and goes through M0.
+// Issued as inline asm so that the compiler does not order every later LDS
+// read behind them: the kernel makes them visible itself, with an explicit
+// vmcnt(0) wait before the barrier that publishes a tile (lds_publish).  The
+// kernel never indexes registers dynamically, so the compiler holds nothing
+// in M0 across these statements.
+__device__ __forceinline__ void g2l16(const void* gsrc, const void* lds_base) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gsrc), "s"(la) : "memory", "m0");
+}
+__device__ __forceinline__ void g2l4(const void* gsrc, const void* lds_base) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(gsrc), "s"(la) : "memory", "m0");
+}
+// Wait for this wave's global -> LDS copies, then the workgroup barrier.
+__device__ __forceinline__ void lds_publish() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+// XOR swizzles of the 16-byte chunks of a K row (D bytes) and of a V^T row
+// (64 bytes): the 16 rows read together by one half-wave land in distinct
+// bank groups, without padding.
+template <int D>
+__device__ __forceinline__ int swz_k(int r) { return D == 128 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
+__device__ __forceinline__ int swz_v(int r) { return (r >> 2) & 3; }
 
 // Key held by accumulator row i of a 32-key MFMA block:
 // pi(i) = 16*((i>>2)&1) + 4*(i>>3) + (i&3); kperm_inv is its inverse.
@@ -244,17 +276,18 @@ __device__ __forceinline__ void blasst_fill_values(const KArgs& a, const float (
 }
 
 template <int D, bool QK_MX, int P_MODE, int RB, bool BLASST, bool VALPHA>
-__global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(const KArgs a) {
+__global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd_kernel(const KArgs a) {
   constexpr int NH = D / 64;          // 64-wide contraction halves of D
   constexpr int NDB = D / 32;         // 32-row blocks of O^T
-  constexpr int KR = D + 16;          // LDS row pitch of K (bytes)
   constexpr int CPT = kTN * D / 16 / kThreads;  // 16-byte chunks per thread per K (and V) tile
   constexpr bool HAS_BIAS = RB != RB_ONLINE;
   constexpr bool HAS_EST = RB == RB_EST_BIAS;
 
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[2][kTN * KR];
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[2][D * kVR];
-  __shared__ __attribute__((aligned(16))) TileMeta<D> meta[2];
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds[2][kTN * D];   // swizzled K rows (key order kperm)
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds[2][D * kTN];   // swizzled V^T rows
+  __shared__ __attribute__((aligned(16))) uint32_t ke_lds[2][kTN];  // MX: E8M0 bytes of the key's D/32 chunks
+  __shared__ __attribute__((aligned(16))) KMeta kmeta[2];
+  __shared__ __attribute__((aligned(16))) VMeta<D> vmeta[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -324,142 +357,138 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(const KArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) cacc[db][r] = 0.0f;
 
-  // ---- tile loader: K / V^T chunks + metadata, prefetched one tile ahead -------
-  // thread's 16-byte chunks of a tile: global offsets and LDS destinations
-  // (K rows permuted by kperm within each 32-key block)
-  uint4 kr0, kr1, vr0, vr1;
-  int kofs0, kofs1 = 0, vofs0, vofs1 = 0, klds0, klds1 = 0, vlds0, vlds1 = 0;
-  {
-    auto chunk = [&](int c, int& kofs, int& vofs, int& klds, int& vlds) {
-      const int e = tid + c * kThreads;
-      const int n = e / (D / 16), ch = e % (D / 16);
-      kofs = n * D + ch * 16;
-      klds = (32 * (n >> 5) + kperm_inv(n & 31)) * KR + ch * 16;
-      const int d = e / (kTN / 16), cv = e % (kTN / 16);
-      vofs = d * P + cv * 16;
-      vlds = d * kVR + cv * 16;
-    };
-    chunk(0, kofs0, vofs0, klds0, vlds0);
-    if constexpr (CPT == 2) chunk(1, kofs1, vofs1, klds1, vlds1);
+  // ---- tile loader ------------------------------------------------------------
+  // K codes (and MX K scales) are staged two tiles ahead -- the scores of tile
+  // t+1 are computed while the softmax of tile t runs -- V codes and the other
+  // metadata one tile ahead.  All copies go global -> LDS directly (no
+  // registers); each thread owns CPT 16-byte chunks of the K and V^T tiles.
+  // LDS chunk slot s of the K tile is (row s / (D/16), physical chunk s % (D/16));
+  // row r holds key 32*(r/32) + kperm(r%32), so that the MFMA accumulator rows
+  // come out in the lane's key order.  V^T rows are the D columns of V.
+  int kofs[CPT], vofs[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int sl = c * kThreads + tid;
+    const int r = sl / (D / 16), ch = (sl % (D / 16)) ^ swz_k<D>(sl / (D / 16));
+    kofs[c] = (32 * (r >> 5) + kperm(r & 31)) * D + ch * 16;
+    const int d = sl / (kTN / 16), cv = (sl % (kTN / 16)) ^ swz_v(sl / (kTN / 16));
+    vofs[c] = d * P + cv * 16;
   }
-  float mb = 0.0f, ma = 0.0f;
-  uint32_t mk = 0, mv = 0;
-  const int ld_w = tid >> 6, ld_k = tid & 63;
   int bias_grp = 0;
   if constexpr (HAS_BIAS) {
-    bias_grp = (qb * kQB + ld_w * 32) >> a.lg_qgroup;
+    bias_grp = (qb * kQB + wave * 32) >> a.lg_qgroup;
     if (bias_grp >= a.G) bias_grp = a.G - 1;
   }
   const float* bias_src = HAS_BIAS ? a.bias + (static_cast<size_t>(bh) * a.G + bias_grp) * P : nullptr;
-
-#define LBFQ_LOAD_TILE(IT)                                                                          \
-  {                                                                                                 \
-    const int key0_ = (IT) * kTN;                                                                   \
-    kr0 = *reinterpret_cast<const uint4*>(kbase + key0_ * D + kofs0);                              \
-    vr0 = *reinterpret_cast<const uint4*>(vbase + key0_ + vofs0);                                   \
-    if constexpr (CPT == 2) {                                                                       \
-      kr1 = *reinterpret_cast<const uint4*>(kbase + key0_ * D + kofs1);                            \
-      vr1 = *reinterpret_cast<const uint4*>(vbase + key0_ + vofs1);                                 \
-    }                                                                                               \
-    if constexpr (HAS_BIAS) mb = bias_src[key0_ + ld_k];                                            \
-    if constexpr (QK_MX) {                                                                          \
-      if (tid < kTN) {                                                                              \
-        const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_scale) +                           \
-                            (static_cast<size_t>(bh) * P + key0_ + tid) * (D / 32);                 \
-        mk = D == 128 ? *reinterpret_cast<const uint32_t*>(kp) : *reinterpret_cast<const uint16_t*>(kp); \
-      }                                                                                             \
-    } else {                                                                                        \
-      if (tid < 4) {                                                                                \
-        int kb_ = (key0_ + 16 * tid) >> a.lg_qkblk;                                                 \
-        kb_ = kb_ < a.nqkblk ? kb_ : a.nqkblk - 1;                                                  \
-        mk = __float_as_uint(reinterpret_cast<const float*>(a.k_scale)[bh * a.nqkblk + kb_]);       \
-      }                                                                                             \
-    }                                                                                               \
-    if (a.v_kind == 1) {                                                                            \
-      if (tid == 0) mv = __float_as_uint(reinterpret_cast<const float*>(a.v_scale)[bh * a.nvblk + (key0_ >> a.lg_vblk)]); \
-    } else if (a.v_kind == 2) {                                                                     \
-      if (tid < D / 4)                                                                              \
-        mv = reinterpret_cast<const uint32_t*>(a.v_scale)[((bh * a.nvblk + (key0_ >> a.lg_vblk)) * D) / 4 + tid]; \
-    }                                                                                               \
-    if constexpr (VALPHA) {                                                                         \
-      if (tid < D) ma = a.v_alpha[(static_cast<size_t>(bh) * a.nvsb + (key0_ >> a.lg_vsb)) * D + tid]; \
-    }                                                                                               \
-  }
-#define LBFQ_STORE_TILE(BUF)                                                                        \
-  {                                                                                                 \
-    *reinterpret_cast<uint4*>(&k_lds[BUF][klds0]) = kr0;                                            \
-    *reinterpret_cast<uint4*>(&v_lds[BUF][vlds0]) = vr0;                                            \
-    if constexpr (CPT == 2) {                                                                       \
-      *reinterpret_cast<uint4*>(&k_lds[BUF][klds1]) = kr1;                                          \
-      *reinterpret_cast<uint4*>(&v_lds[BUF][vlds1]) = vr1;                                          \
-    }                                                                                               \
-    if constexpr (HAS_BIAS) meta[BUF].bias[ld_w][ld_k] = mb;                                        \
-    if constexpr (QK_MX) {                                                                          \
-      if (tid < kTN) meta[BUF].ke[tid] = mk;                                                        \
-    } else {                                                                                        \
-      if (tid < 4) meta[BUF].ksc[tid] = __uint_as_float(mk);                                        \
-    }                                                                                               \
-    if (a.v_kind == 1) {                                                                            \
-      if (tid == 0) meta[BUF].vsc = __uint_as_float(mv);                                            \
-    } else if (a.v_kind == 2) {                                                                     \
-      if (tid < D / 4) meta[BUF].ve[tid] = mv;                                                      \
-    }                                                                                               \
-    if constexpr (VALPHA) {                                                                         \
-      if (tid < D) meta[BUF].valpha[tid] = ma;                                                      \
-    }                                                                                               \
-  }
-
   const int nt = (S + kTN - 1) / kTN;
-  LBFQ_LOAD_TILE(0)
-  LBFQ_STORE_TILE(0)
-  __syncthreads();
+  // V^T E8M0 column scales are constant 127 (= 1) unless V is MX
+  if (a.v_kind != 2 && tid < D / 4) {
+    vmeta[0].ve[tid] = 0x7f7f7f7fu;
+    vmeta[1].ve[tid] = 0x7f7f7f7fu;
+  }
 
-  const bool pv_scaled = (a.v_kind == 2) || (P_MODE == 1);
-
-  for (int it = 0; it < nt; ++it) {
-    const int cur = it & 1;
-    if (it + 1 < nt) LBFQ_LOAD_TILE(it + 1)
+  auto load_k = [&](int it, int buf) {
+    const uint8_t* src = kbase + (it * kTN) * D;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) g2l16(src + kofs[c], &k_lds[buf][(c * kThreads + wave * 64) * 16]);
+    if constexpr (QK_MX) {
+      // E8M0 bytes of the 64 keys (D/32 per key), one dword per lane
+      const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_scale) + (static_cast<size_t>(bh) * P + it * kTN) * (D / 32);
+      if (wave == 0 && lane < kTN * (D / 32) / 4) g2l4(kp + 4 * lane, &ke_lds[buf][0]);
+    }
+  };
+  auto load_v = [&](int it, int buf) {
     const int key0 = it * kTN;
-    const TileMeta<D>& tm = meta[cur];
-
-    // ---- S^T = K Q^T ------------------------------------------------------------
-    v16f s[2];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) g2l16(vbase + key0 + vofs[c], &v_lds[buf][(c * kThreads + wave * 64) * 16]);
+    if constexpr (HAS_BIAS) g2l4(bias_src + key0 + lane, &kmeta[buf].bias[wave][0]);
+    if constexpr (!QK_MX) {
+      if (wave == 1 && lane < 4) {
+        int kb = (key0 + 16 * lane) >> a.lg_qkblk;
+        kb = kb < a.nqkblk ? kb : a.nqkblk - 1;
+        g2l4(reinterpret_cast<const float*>(a.k_scale) + bh * a.nqkblk + kb, &kmeta[buf].ksc[0]);
+      }
+    }
+    const int vblk = bh * a.nvblk + (key0 >> a.lg_vblk);
+    if (a.v_kind == 1) {
+      if (wave == 2 && lane == 0) g2l4(reinterpret_cast<const float*>(a.v_scale) + vblk, &vmeta[buf].vsc);
+    } else if (a.v_kind == 2) {
+      if (wave == 2 && lane < D / 4)
+        g2l4(reinterpret_cast<const uint32_t*>(a.v_scale) + vblk * (D / 4) + lane, &vmeta[buf].ve[0]);
+    }
+    if constexpr (VALPHA) {
+      const float* va = a.v_alpha + (static_cast<size_t>(bh) * a.nvsb + (key0 >> a.lg_vsb)) * D;
+      if (wave == 3) {
+#pragma unroll
+        for (int c = 0; c < D / 64; ++c) g2l4(va + 64 * c + lane, &vmeta[buf].valpha[64 * c]);
+      }
+    }
+  };
+  // S^T = K Q^T of the K tile in buffer kb
+  auto scores = [&](int kb, v16f (&s)[2]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[t][r] = 0.0f;
 #pragma unroll
       for (int hh = 0; hh < NH; ++hh) {
-        const uint8_t* rp = &k_lds[cur][(32 * t + li) * KR + 64 * hh + 16 * g];
-        v8i ka = lds_read32(rp, rp + 32);
+        const int r = 32 * t + li;
+        const uint8_t* rp = &k_lds[kb][r * D];
+        v8i ka = lds_read32(rp + 16 * ((4 * hh + g) ^ swz_k<D>(r)), rp + 16 * ((4 * hh + 2 + g) ^ swz_k<D>(r)));
         if constexpr (QK_MX) {
-          int ke = (tm.ke[32 * t + kperm(li)] >> (8 * (2 * hh + g))) & 0xff;
+          int ke;
+          if constexpr (D == 128) ke = (ke_lds[kb][32 * t + kperm(li)] >> (8 * (2 * hh + g))) & 0xff;
+          else ke = reinterpret_cast<const uint8_t*>(&ke_lds[kb][0])[2 * (32 * t + kperm(li)) + g];
           s[t] = mfma32<true>(ka, qop[hh], s[t], ke, qe[hh]);
         } else {
           s[t] = mfma32<false>(ka, qop[hh], s[t], 0, 0);
         }
       }
     }
+  };
+
+  // prologue: tile 0 complete, K codes of tile 1
+  load_k(0, 0);
+  load_v(0, 0);
+  load_k(nt > 1 ? 1 : 0, 1);
+  lds_publish();
+  v16f s_a[2], s_b[2];
+  scores(0, s_a);
+  __syncthreads();  // every wave has read K tile 0 before it is overwritten
+
+  // one K/V tile: softmax of s_cur (tile it) while the scores of tile it+1
+  // are computed into s_nxt
+  auto step = [&](const int it, v16f (&s_cur)[2], v16f (&s_nxt)[2]) __attribute__((always_inline)) {
+    const int cur = it & 1;
+    const int key0 = it * kTN;
+    // global -> LDS prefetch: K of tile it+2 into the buffer of tile it (read
+    // before the last barrier), V and metadata of tile it+1 (clamped: the last
+    // iterations reload the last tile into buffers nobody reads any more)
+    load_k(it + 2 < nt ? it + 2 : nt - 1, cur);
+    load_v(it + 1 < nt ? it + 1 : nt - 1, 1 - cur);
+    // scores of the next tile run on the matrix cores during this softmax
+    if (it + 1 < nt) scores(1 - cur, s_nxt);
+    const KMeta& km = kmeta[cur];
 
     // ---- scores in log2 units: u = dot * C (+ qm correction), masked ------------
     float u[32];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       float C = qC;
-      if constexpr (!QK_MX) C *= tm.ksc[2 * t + g];
+      if constexpr (!QK_MX) C *= km.ksc[2 * t + g];
       if constexpr (HAS_BIAS) {
-        const float4* bp = reinterpret_cast<const float4*>(&tm.bias[wave][32 * t + 16 * g]);
+        const float4* bp = reinterpret_cast<const float4*>(&km.bias[wave][32 * t + 16 * g]);
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           float4 bb = bp[q4];
-          u[16 * t + 4 * q4 + 0] = fmaf(s[t][4 * q4 + 0], C, bb.x);
-          u[16 * t + 4 * q4 + 1] = fmaf(s[t][4 * q4 + 1], C, bb.y);
-          u[16 * t + 4 * q4 + 2] = fmaf(s[t][4 * q4 + 2], C, bb.z);
-          u[16 * t + 4 * q4 + 3] = fmaf(s[t][4 * q4 + 3], C, bb.w);
+          u[16 * t + 4 * q4 + 0] = fmaf(s_cur[t][4 * q4 + 0], C, bb.x);
+          u[16 * t + 4 * q4 + 1] = fmaf(s_cur[t][4 * q4 + 1], C, bb.y);
+          u[16 * t + 4 * q4 + 2] = fmaf(s_cur[t][4 * q4 + 2], C, bb.z);
+          u[16 * t + 4 * q4 + 3] = fmaf(s_cur[t][4 * q4 + 3], C, bb.w);
         }
       } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) u[16 * t + r] = s[t][r] * C;
+        for (int r = 0; r < 16; ++r) u[16 * t + r] = s_cur[t][r] * C;
       }
     }
     if (key0 + kTN > S) {
@@ -516,7 +545,7 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(const KArgs a) {
       } else {
         const float ra = fast_exp2(bmax - m_new);
         const bool floored = !(ra > 1e-12f);
-        s_lp = (floored ? 1e-12f : ra) / kFp8Max;
+        s_lp = (floored ? 1e-12f : ra) * (1.0f / kFp8Max);
         T = (floored ? m_new + kLog2DynFloor : bmax) - kLog2Fp8Max;
         sig_p = s_lp;
       }
@@ -588,28 +617,26 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(const KArgs a) {
     }
 
     // ---- accumulator rescale (alpha, dynamic P scale, fp8_block V scale) ---------
+    const VMeta<D>& vm = vmeta[cur];
     float sig_new = sig_p;
-    if (a.v_kind == 1) sig_new *= tm.vsc;
-    const float f = alpha * (sigma / sig_new);
+    if (a.v_kind == 1) sig_new *= vm.vsc;
+    const float f = alpha * sigma * __builtin_amdgcn_rcpf(sig_new);
     sigma = sig_new;
-    if (__any(f != 1.0f)) {
+    if (P_MODE == 2 || __any(f != 1.0f)) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] *= f;
     }
 
-    // ---- O^T += V^T P^T -----------------------------------------------------------
+    // ---- O^T += V^T P^T (E8M0 scales: MX V columns, MX P; 127 = 1 otherwise) -------
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      const uint8_t* vp = &v_lds[cur][(32 * db + li) * kVR + 16 * g];
-      v8i va = lds_read32(vp, vp + 32);
-      if (pv_scaled) {
-        int ve = a.v_kind == 2 ? static_cast<int>((tm.ve[(32 * db + li) >> 2] >> (8 * (li & 3))) & 0xff) : 127;
-        acc[db] = mfma32<true>(va, pop, acc[db], ve, pe);
-      } else {
-        acc[db] = mfma32<false>(va, pop, acc[db], 0, 0);
-      }
+      const int r = 32 * db + li;
+      const uint8_t* vp = &v_lds[cur][r * kTN];
+      v8i va = lds_read32(vp + 16 * (g ^ swz_v(r)), vp + 16 * ((2 + g) ^ swz_v(r)));
+      const int ve = static_cast<int>((vm.ve[(32 * db + li) >> 2] >> (8 * (li & 3))) & 0xff);
+      acc[db] = mfma32<true>(va, pop, acc[db], ve, pe);
     }
 
     // ---- V-smoothing accumulator: c = c * alpha + rowsum(P_deq) (x) alpha_v -------
@@ -627,19 +654,18 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(const KArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int d = 32 * db + 8 * (r >> 2) + 4 * g + (r & 3);
-          cacc[db][r] = fmaf(rs, tm.valpha[d], cacc[db][r] * alpha);
+          cacc[db][r] = fmaf(rs, vm.valpha[d], cacc[db][r] * alpha);
         }
     }
     m2 = m_new;
 
-    // keep the next tile's LDS stores (and so the wait for its global loads)
-    // after this tile's compute
-    __asm__ volatile("" ::: "memory");
-    if (it + 1 < nt) LBFQ_STORE_TILE(1 - cur)
-    __syncthreads();
+    lds_publish();
+  };
+  for (int it = 0; it < nt; ++it) {
+    step(it, s_a, s_b);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) s_a[t] = s_b[t];
   }
-#undef LBFQ_LOAD_TILE
-#undef LBFQ_STORE_TILE
 
   // ---- epilogue ---------------------------------------------------------------------
   const float lfull = xor32_add(l);
