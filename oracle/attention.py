@@ -26,11 +26,17 @@ bf16 V (mxfp8), exactly as the reference marshals them
 (``attention.py:554-575``).  ``rows`` restricts the computation to a subset
 of query rows (used for the bounded CPU baseline sample).
 
-Pinned by ``tests/test_oracle_attention.py``: against a dense brute-force
-softmax at tiny S (online row max, P quant off-by-construction cases), the
-reference tests' own torch mirrors restated (``tests/test_triton_attn.py``
-of the reference), mx-P independence of ``p_max_offset`` (bitwise), qm_k vs
-online agreement for dynamic P, V-smoothing accumulator == un-smoothed V.
+Pinned by ``tests/test_oracle_attention.py`` with checks that do not restate
+these formulas: on inputs whose log2-unit scores are integers every P value is
+a power of two and exactly representable in all three P modes, so the
+streaming loop must reproduce a dense float64 softmax (online row max, rising
+row max, qm correction, fixed and dynamic qm_k estimates with both threshold
+moves, fp8_block V scales, V smoothing, ragged S); V smoothing equals attention
+on V + alpha (linearity, non-exact P); mx P is bitwise independent of
+``p_max_offset`` (reference test_v_quant_variants.py:337-356); BLASST fills
+reproduce the exact p on constant-score key blocks, zero / thr fills and skip
+statistics match closed forms on a block layout whose skip set is known; the
+qm_k estimate equals a brute-force maximum.
 """
 
 from __future__ import annotations

@@ -12,6 +12,12 @@ Follows ``attention.py`` of the reference:
 * ``fake_quant_attention`` -- ``attention.py:706-806`` (guards, inverse Q gather).
 
 ``cfg`` is any object with the ``QuantConfig`` fields.  All tensors are CPU.
+
+Pinned by ``tests/test_oracle_pipeline.py``: Q k-means reorder + inverse gather
+is a bitwise row permutation when per-row MX scales make quantisation
+order-independent; V k-means with the K co-permutation only reorders the key
+sum under a fixed row max; the SDPA path equals torch SDPA on the dequantised
+tensors.  The functions it composes are pinned in their own modules.
 """
 
 from __future__ import annotations
