@@ -58,25 +58,17 @@ def _events_time(fn, iters: int, warmup: int) -> float:
 
 
 def cpu_baseline_and_error(q, k, v, cfg, out_gpu, n_real, rows_sample, sm_scale):
-    """Oracle on head 0: full preprocess/quant, attention for a row sample.
-    Returns (cpu_baseline dict, error dict)."""
-    from oracle import attention as oattn
+    """The CPU oracle of the reference path on head 0: preprocess (untimed), then
+    the P-requant path -- quantise the head, row-max estimate, streaming
+    attention -- for a bounded sample of query rows (timed; the reference's
+    timing likewise includes quant/dequant and excludes the cached preprocess,
+    bench/eval_wan21.py:208-255).  Returns (cpu_baseline dict, error dict)."""
     from oracle import pipeline as opipe
     q0, k0, v0 = (t[:, :, :1].contiguous() for t in (q, k, v))
     b, s, h, d = q0.shape
     t0 = time.time()
     qw, kw, vw, qm, v_alpha, q_km, _ = opipe.preprocess(q0, k0, v0, cfg)
-    qi, ki = opipe.qk_quant_inputs(qw, kw, cfg)
-    qc, qs, qmeta = opipe.quant_qk(qi, cfg)
-    kc, ks, kmeta = opipe.quant_qk(ki, cfg)
-    q_deq = opipe.dequant_qk(qc, qs, qmeta, torch.bfloat16)
-    k_deq = opipe.dequant_qk(kc, ks, kmeta, torch.bfloat16)
-    vc, vs, vmeta = opipe.quant_v(vw, cfg)
-    from oracle import quant as oq
-    v_bf = oq.decode(vc).to(torch.bfloat16)
-    rowmax = oattn.estimate_rowmax_qm_k(qm, kw, block_q=cfg.q_smooth_block_size, sm_scale=sm_scale)
     prep_s = time.time() - t0
-    perm = (0, 2, 1, 3)
     # sample reordered rows that map to real (unpadded) original rows
     order = q_km["order"][0] if q_km is not None else torch.arange(s)
     gen = torch.Generator().manual_seed(1)
@@ -84,25 +76,37 @@ def cpu_baseline_and_error(q, k, v, cfg, out_gpu, n_real, rows_sample, sm_scale)
     rows = cand[torch.randperm(len(cand), generator=gen)[:rows_sample]].sort().values
     nthreads = torch.get_num_threads()
     t1 = time.time()
-    o = oattn.attention(q_deq.permute(*perm).contiguous(), k_deq.permute(*perm).contiguous(),
-                        v_bf.permute(*perm).contiguous(), vs.float(), sm_scale=sm_scale,
-                        p_max_offset=cfg.p_max_offset, block_m=64, block_n=64,
-                        k_smooth=kw.to(torch.bfloat16).permute(*perm).contiguous(), qm=qm.float(),
-                        q_smooth_block=cfg.q_smooth_block_size, p_quant_mode="dynamic", rowmax_est=rowmax,
-                        rows=rows)
+    o = opipe.p_requant_path(qw, kw, vw, qm, v_alpha, cfg, sm_scale, torch.bfloat16, rows=rows)
     attn_s = time.time() - t1
     flops = 4.0 * len(rows) * s * d
     gpu_rows = out_gpu[0, order[rows], 0].float().cpu()
-    ref_rows = o[0, 0].float()
+    ref_rows = o[0, :, 0].float()
     cos = torch.nn.functional.cosine_similarity(gpu_rows.flatten().unsqueeze(0), ref_rows.flatten().unsqueeze(0)).item()
-    mx = (gpu_rows - ref_rows).abs().max().item()
+    diff = (gpu_rows - ref_rows).abs()
+    ulp = torch.pow(2.0, torch.floor(torch.log2(ref_rows.abs().clamp_min(2.0 ** -126))) - 7)
     cpu = {"value": flops / attn_s / 1e12, "unit": "TFLOP/s", "cores": nthreads, "kind": "port",
-           "sample": f"oracle attention, head 0, {len(rows)} query rows x {s} keys, D={d}, fp32 torch on "
-                     f"{nthreads} threads ({attn_s:.1f} s; oracle prepass of the head {prep_s:.1f} s not timed)",
+           "sample": f"oracle P-requant path (quantise head 0, row-max estimate, streaming attention) for "
+                     f"{len(rows)} query rows x {s} keys, D={d}, fp32 torch on {nthreads} threads "
+                     f"({attn_s:.1f} s; the head's preprocess, {prep_s:.1f} s, not timed)",
            "seconds": attn_s}
-    err = {"cos": cos, "max_abs": mx, "rows": len(rows), "head": 0,
+    err = {"cos": cos, "max_abs": diff.max().item(),
+           "max_abs_beyond_1_bf16_ulp": (diff - ulp).clamp_min(0).max().item(),
+           "frac_gt_1e-2": (diff > 1e-2).float().mean().item(), "rows": len(rows), "head": 0,
            "vs": "CPU oracle of the reference path (not SDPA)"}
     return cpu, err
+
+
+def traffic_from_profile(config: int):
+    """HBM bytes per attention launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated by a copy of known size), or None."""
+    import glob
+    import re
+    for path in sorted(glob.glob(os.path.join(REPO, "profiles", f"traffic_attn_fwd_c{config}_*.md"))):
+        with open(path) as f:
+            m = re.search(r"^hbm_bytes_per_launch:\s*(\d+)", f.read(), flags=re.M)
+        if m:
+            return int(m.group(1))
+    return None
 
 
 def main() -> int:
@@ -112,8 +116,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--heads", type=int, default=0, help="override H (debug)")
-    ap.add_argument("--cpu-rows", type=int, default=512)
+    ap.add_argument("--cpu-rows", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="driver for rocprofv3 --pmc passes: a 1 GiB calibration copy, then one attention launch")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU per process; --gpus N>1 is not supported "
@@ -148,6 +154,19 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"prepass: preprocess {prep_ms:.3f} ms, quantise+qmk {quant_ms:.3f} ms")
 
+    if args.pmc_pass:
+        # a plain copy of known size (2^30 bytes read, 2^30 written) calibrates
+        # FETCH_SIZE / WRITE_SIZE; then exactly one attention launch
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        launch_attention(ops, cfg, sm_scale, torch.bfloat16)
+        torch.cuda.synchronize()
+        log("pmc pass: calibration copy + one attention launch done")
+        return 0
+
     # ---- attention kernel: the timed step ----------------------------------
     out = launch_attention(ops, cfg, sm_scale, torch.bfloat16)
     torch.cuda.synchronize()
@@ -177,20 +196,14 @@ def main() -> int:
 
     cpu_baseline = None
     err = None
-    if not args.no_cpu and args.config in (1, 2):
+    if not args.no_cpu and args.config in (1, 2, 3):
         log("cpu baseline / error sample ...")
         cpu_baseline, err = cpu_baseline_and_error(q, k, v, cfg, out, n_real, args.cpu_rows, sm_scale)
 
     roof = {"bound": "mfma", "achieved": tflops, "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": tflops / FP8_PEAK_TFLOPS, "traffic": None,
             "kernel": "attn_fwd_kernel", "flops_per_launch": flops}
-    tp = os.path.join(REPO, "profiles", f"traffic_attention_c{args.config}.json")
-    if os.path.exists(tp):
-        try:
-            with open(tp) as f:
-                roof["traffic"] = json.load(f).get("hbm_bytes_per_launch")
-        except Exception:  # noqa: BLE001
-            pass
+    roof["traffic"] = traffic_from_profile(args.config)
     line = {
         "metric": "attn TFLOPS & % FP8-MFMA peak at 40h x 32760 x d128; prepass HBM GB/s; err vs ref",
         "value": tflops,

@@ -114,10 +114,12 @@ int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64
  *   bias[b,h,g,n]   = (qm[b,g,h,:] . K_s[b,n,h,:]) * scale       (fp32)
  *   rowmax[b,h,g]   = max_n bias[b,h,g,n]
  * (the attention path passes scale = sm_scale * log2(e): scores in log2 units)
- * K_s is NHD (dtype) optionally gathered by `gather` (V-kmeans order).
- * bias is (B,H,G,s_pitch) (NULL to skip), rowmax (B,H,G) (NULL to skip). */
-int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, int64_t B, int64_t S,
-             int64_t H, int64_t D, int64_t G, float scale, float* bias, int64_t s_pitch, float* rowmax,
+ * K_s = round_to_dtype(ks[gather[n]] - ks_mean) when ks_mean (B,H,D) fp32 is
+ * given (ks is then the raw NHD K), else ks itself (already smoothed); gather
+ * (the V-kmeans order) may be NULL.  bias is (B,H,G,s_pitch) (NULL to skip),
+ * rowmax (B,H,G) (NULL to skip). */
+int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, const float* ks_mean, int64_t B,
+             int64_t S, int64_t H, int64_t D, int64_t G, float scale, float* bias, int64_t s_pitch, float* rowmax,
              lbfq_stream_t stream);
 
 /* ---- FP8-MFMA P-requant attention ------------------------------------------

@@ -8,7 +8,8 @@
 //
 // Work decomposition: one workgroup = 4 waves = 128 queries of one (b, h);
 // each wave owns 32 queries.  K and V^T tiles of 64 keys (== the reference
-// block_n) are staged in LDS, double buffered, together with the per-tile
+// block_n) are copied global -> LDS directly (three-slot K ring, four-slot
+// V^T ring, staged three and two tiles ahead) together with the per-tile
 // metadata (qm correction row, K/V scales, V block means), and shared by the
 // 4 waves.  Scores are computed transposed, S^T = K Q^T, so every lane owns
 // exactly one query: lane l holds query l % 32 and, in lane group
@@ -35,7 +36,21 @@
 // Per-query fp32 factors of the accumulator (online-softmax alpha, dynamic P
 // scale, fp8_block V scale) are folded into one rescale of O^T per tile,
 // skipped when the whole wave has factor 1.
+//
+// Schedule of one tile step (per wave): the softmax of tile t runs in four
+// chunks of 8 keys per lane; each chunk carries one or two MFMAs that do not
+// depend on it -- the PV of tile t-1 (P codes kept in registers) and the QK of
+// tile t+1 (written into score registers the earlier chunks have consumed).
+// On gfx950 a 32x32x64 MFMA blocks most VALU issue of its SIMD while it runs,
+// so a tile costs roughly its VALU cycles plus about half of its MFMA cycles;
+// the interleave keeps the wave from idling on its own LDS reads and MFMA
+// results.  Empty asm fences (pin / use) and sched_barrier keep each chunk's
+// work together, and all LDS reads of a step are issued before the first
+// instruction that waits on any of them.
 #pragma once
+
+#include <cstddef>
+#include <type_traits>
 
 #include "lbfq_common.h"
 #include "../../include/lbfq.h"
@@ -88,17 +103,33 @@ struct KArgs {
 // consumed by the softmax of the tile, the V side by its PV product.
 struct KMeta {
   float bias[kWaves][kTN];  // qm correction (log2 units) of each wave's group
-  float ksc[4];             // fp8_block K scale of each 16-key group
+  uint32_t ke[kTN];         // MX: E8M0 bytes of the keys' D/32 chunks
+  float ksc[kTN];           // fp8_block: scale of the 16-key group of each key
 };
 
 template <int D>
 struct VMeta {
-  uint32_t ve[D / 4];       // E8M0 byte of each V column (4 per word); 127 unless V is MX
-  float vsc;                // fp8_block V scale of the tile
+  uint32_t ve[kTN];         // E8M0 byte of each V column (4 per word, D/4 words); 127 unless V is MX
   float valpha[D];          // V block mean of the tile
+  float vsc[kTN];           // fp8_block V scale of the tile (all entries equal)
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Hardware max of raw scores.  fmaxf on a value the compiler cannot prove
+// canonical (an MFMA result, a lane exchange, a loop-carried value) costs an
+// extra v_max x, x, x each; the scores here are finite or -inf, for which the
+// plain instructions are exact.
+__device__ __forceinline__ float hmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float hmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 
 template <bool SCALED>
 __device__ __forceinline__ v16f mfma32(const v8i& a, const v8i& b, const v16f& c, int sa, int sb) {
@@ -123,17 +154,45 @@ __device__ __forceinline__ v8i lds_read32(const uint8_t* p0, const uint8_t* p1) 
 // vmcnt(0) wait before the barrier that publishes a tile (lds_publish).  The
 // kernel never indexes registers dynamically, so the compiler holds nothing
 // in M0 across these statements.
-__device__ __forceinline__ void g2l16(const void* gsrc, const void* lds_base) {
-  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base)));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gsrc), "s"(la) : "memory", "m0");
+// Addressing: wave-uniform 64-bit global base (SGPRs) + per-lane 32-bit byte
+// offset, LDS base as a wave-uniform byte address.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
 }
-__device__ __forceinline__ void g2l4(const void* gsrc, const void* lds_base) {
-  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base)));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(gsrc), "s"(la) : "memory", "m0");
+__device__ __forceinline__ void g2l16(const void* gbase, uint32_t vofs, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(vofs), "s"(gbase), "s"(lds_base)
+               : "memory", "m0");
 }
-// Wait for this wave's global -> LDS copies, then the workgroup barrier.
+__device__ __forceinline__ void g2l4(const void* gbase, uint32_t vofs, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(vofs), "s"(gbase), "s"(lds_base)
+               : "memory", "m0");
+}
+// Scheduling fences for register values (no instruction is emitted): pin(x)
+// makes x look redefined here, so work that reads it cannot start earlier;
+// use(x) makes x look read here, so the work that produces it cannot sink
+// below.  Between sched_barrier(0) fences they hold a chunk of independent
+// VALU and MFMA work together, so one wave issues both side by side.
+// (The host pass type-checks device code too and has no "v" registers.)
+template <typename T>
+__device__ __forceinline__ void pin(T& x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("" : "+v"(x));
+#endif
+}
+template <typename T>
+__device__ __forceinline__ void use(const T& x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("" ::"v"(x));
+#endif
+}
+
+// Wait until at most N of this wave's global -> LDS copies are in flight (the
+// ones issued during the current tile), then the workgroup barrier: every
+// copy issued one tile earlier has landed for every wave.
+template <int N>
 __device__ __forceinline__ void lds_publish() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);  // vmcnt(N), expcnt / lgkmcnt unconstrained
   __syncthreads();
 }
 
@@ -149,8 +208,18 @@ __device__ __forceinline__ int swz_v(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ int kperm(int i) { return 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3); }
 __device__ __forceinline__ int kperm_inv(int k) { return 8 * ((k >> 2) & 3) + 4 * (k >> 4) + (k & 3); }
 
-__device__ __forceinline__ float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
-__device__ __forceinline__ float xor32_add(float v) { return v + __shfl_xor(v, 32, 64); }
+// Combine lane l with lane l ^ 32: v_permlane32_swap exchanges the upper half
+// of its first operand with the lower half of its second, so (r0, r1) hold
+// (v[l], v[l^32]) in one order or the other, and max / sum of the pair is the
+// same in both halves of the wave.
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return hmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_add(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // ---- BLASST fill values (attention_triton.py:231-324) in the lane layout -----
 // u: scores in log2 units (-inf where masked); p units include the elementwise
@@ -283,11 +352,12 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
   constexpr bool HAS_BIAS = RB != RB_ONLINE;
   constexpr bool HAS_EST = RB == RB_EST_BIAS;
 
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[2][kTN * D];   // swizzled K rows (key order kperm)
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[2][D * kTN];   // swizzled V^T rows
-  __shared__ __attribute__((aligned(16))) uint32_t ke_lds[2][kTN];  // MX: E8M0 bytes of the key's D/32 chunks
-  __shared__ __attribute__((aligned(16))) KMeta kmeta[2];
-  __shared__ __attribute__((aligned(16))) VMeta<D> vmeta[2];
+  // rings: K tile i lives in slot i % 3, V^T tile i in slot i % 4
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds[3][kTN * D];   // swizzled K rows (key order kperm)
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds[4][D * kTN];   // swizzled V^T rows
+  __shared__ __attribute__((aligned(16))) KMeta kmeta[3];
+  __shared__ __attribute__((aligned(16))) VMeta<D> vmeta[4];
+  __shared__ __attribute__((aligned(16))) float binit[HAS_BIAS ? kWaves : 1][2][kTN];  // bias / C per query half
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -358,14 +428,14 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     for (int r = 0; r < 16; ++r) cacc[db][r] = 0.0f;
 
   // ---- tile loader ------------------------------------------------------------
-  // K codes (and MX K scales) are staged two tiles ahead -- the scores of tile
-  // t+1 are computed while the softmax of tile t runs -- V codes and the other
-  // metadata one tile ahead.  All copies go global -> LDS directly (no
-  // registers); each thread owns CPT 16-byte chunks of the K and V^T tiles.
-  // LDS chunk slot s of the K tile is (row s / (D/16), physical chunk s % (D/16));
-  // row r holds key 32*(r/32) + kperm(r%32), so that the MFMA accumulator rows
-  // come out in the lane's key order.  V^T rows are the D columns of V.
-  int kofs[CPT], vofs[CPT];
+  // K codes, the qm bias rows and the MX K scales are staged three tiles ahead
+  // (the scores of tile t are computed during tile t-1), V codes, the MX V
+  // column scales and the V block means two tiles ahead, so every copy has a
+  // whole tile of compute to land.  All copies go global -> LDS directly;
+  // every wave issues the same copies with all 64 lanes (the small tables are
+  // copied by every wave, redundantly), so the loop has no lane masks and the
+  // publish wait is a compile-time vmcnt.
+  uint32_t kofs[CPT], vofs[CPT];
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
     const int sl = c * kThreads + tid;
@@ -374,162 +444,276 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     const int d = sl / (kTN / 16), cv = (sl % (kTN / 16)) ^ swz_v(sl / (kTN / 16));
     vofs[c] = d * P + cv * 16;
   }
+  const int nt = (S + kTN - 1) / kTN;
+  // wave-uniform pieces of the copy addresses (SGPRs)
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   int bias_grp = 0;
   if constexpr (HAS_BIAS) {
-    bias_grp = (qb * kQB + wave * 32) >> a.lg_qgroup;
+    bias_grp = (qb * kQB + wv * 32) >> a.lg_qgroup;
     if (bias_grp >= a.G) bias_grp = a.G - 1;
   }
   const float* bias_src = HAS_BIAS ? a.bias + (static_cast<size_t>(bh) * a.G + bias_grp) * P : nullptr;
-  const int nt = (S + kTN - 1) / kTN;
-  // V^T E8M0 column scales are constant 127 (= 1) unless V is MX
-  if (a.v_kind != 2 && tid < D / 4) {
-    vmeta[0].ve[tid] = 0x7f7f7f7fu;
-    vmeta[1].ve[tid] = 0x7f7f7f7fu;
-  }
+  const uint32_t k_lds0 = lds_addr(&k_lds[0][0]), v_lds0 = lds_addr(&v_lds[0][0]);
+  const uint32_t km0 = lds_addr(&kmeta[0]), vm0 = lds_addr(&vmeta[0]);
+  constexpr uint32_t kKBuf = kTN * D, kVBuf = D * kTN;
+  constexpr uint32_t kKMeta = sizeof(KMeta), kVMeta = sizeof(VMeta<D>);
+  const bool v_mx = a.v_kind == 2, v_blk = a.v_kind == 1;
+  constexpr int kCopies = 2 * CPT + (HAS_BIAS ? 1 : 0) + 2 + (VALPHA ? D / 64 : 0);
+  // per-lane byte offsets of the small tables (lanes past a table's end repeat it)
+  const uint32_t ke_lofs = 4 * (lane & (kTN * (D / 32) / 4 - 1));
+  const uint32_t ve_lofs = 4 * (lane & (D / 4 - 1));
+  // V^T column scales are constant 127 (= 1) unless V is MX (then copied per tile)
+  if (!v_mx && tid < 4 * (D / 4)) vmeta[tid / (D / 4)].ve[tid % (D / 4)] = 0x7f7f7f7fu;
 
+  const float* ksc_base = QK_MX ? nullptr : reinterpret_cast<const float*>(a.k_scale) + bh * a.nqkblk;
   auto load_k = [&](int it, int buf) {
-    const uint8_t* src = kbase + (it * kTN) * D;
+    const int key0 = it * kTN;
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) g2l16(src + kofs[c], &k_lds[buf][(c * kThreads + wave * 64) * 16]);
+    for (int c = 0; c < CPT; ++c) g2l16(kbase + key0 * D, kofs[c], k_lds0 + buf * kKBuf + (c * kThreads + wv * 64) * 16);
+    const uint32_t kmb = km0 + buf * kKMeta;
+    if constexpr (HAS_BIAS) g2l4(bias_src + key0, 4 * lane, kmb + wv * kTN * 4);
     if constexpr (QK_MX) {
-      // E8M0 bytes of the 64 keys (D/32 per key), one dword per lane
-      const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_scale) + (static_cast<size_t>(bh) * P + it * kTN) * (D / 32);
-      if (wave == 0 && lane < kTN * (D / 32) / 4) g2l4(kp + 4 * lane, &ke_lds[buf][0]);
+      g2l4(reinterpret_cast<const uint8_t*>(a.k_scale) + (static_cast<size_t>(bh) * P + key0) * (D / 32), ke_lofs,
+           kmb + offsetof(KMeta, ke));
+    } else {
+      // lane l fetches the scale of key l's 16-key group (clamped at the last block)
+      int kb = (key0 + 16 * (lane >> 4)) >> a.lg_qkblk;
+      kb = kb < a.nqkblk ? kb : a.nqkblk - 1;
+      g2l4(ksc_base, 4 * kb, kmb + offsetof(KMeta, ksc));
     }
   };
   auto load_v = [&](int it, int buf) {
     const int key0 = it * kTN;
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) g2l16(vbase + key0 + vofs[c], &v_lds[buf][(c * kThreads + wave * 64) * 16]);
-    if constexpr (HAS_BIAS) g2l4(bias_src + key0 + lane, &kmeta[buf].bias[wave][0]);
-    if constexpr (!QK_MX) {
-      if (wave == 1 && lane < 4) {
-        int kb = (key0 + 16 * lane) >> a.lg_qkblk;
-        kb = kb < a.nqkblk ? kb : a.nqkblk - 1;
-        g2l4(reinterpret_cast<const float*>(a.k_scale) + bh * a.nqkblk + kb, &kmeta[buf].ksc[0]);
-      }
-    }
+    for (int c = 0; c < CPT; ++c) g2l16(vbase + key0, vofs[c], v_lds0 + buf * kVBuf + (c * kThreads + wv * 64) * 16);
+    const uint32_t vmb = vm0 + buf * kVMeta;
+    // one V-side scale copy per tile whatever V carries (no branch): the MX
+    // column scales into ve, the fp8_block scale into vsc, or for per-channel
+    // scales (applied in the epilogue) an unused copy of the first one into vsc
     const int vblk = bh * a.nvblk + (key0 >> a.lg_vblk);
-    if (a.v_kind == 1) {
-      if (wave == 2 && lane == 0) g2l4(reinterpret_cast<const float*>(a.v_scale) + vblk, &vmeta[buf].vsc);
-    } else if (a.v_kind == 2) {
-      if (wave == 2 && lane < D / 4)
-        g2l4(reinterpret_cast<const uint32_t*>(a.v_scale) + vblk * (D / 4) + lane, &vmeta[buf].ve[0]);
-    }
+    const void* vsrc = v_mx ? static_cast<const void*>(reinterpret_cast<const uint32_t*>(a.v_scale) + vblk * (D / 4))
+                            : static_cast<const void*>(reinterpret_cast<const float*>(a.v_scale) + (v_blk ? vblk : 0));
+    g2l4(vsrc, v_mx ? ve_lofs : 0u, vmb + (v_mx ? offsetof(VMeta<D>, ve) : offsetof(VMeta<D>, vsc)));
     if constexpr (VALPHA) {
       const float* va = a.v_alpha + (static_cast<size_t>(bh) * a.nvsb + (key0 >> a.lg_vsb)) * D;
-      if (wave == 3) {
 #pragma unroll
-        for (int c = 0; c < D / 64; ++c) g2l4(va + 64 * c + lane, &vmeta[buf].valpha[64 * c]);
-      }
-    }
-  };
-  // S^T = K Q^T of the K tile in buffer kb
-  auto scores = [&](int kb, v16f (&s)[2]) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[t][r] = 0.0f;
-#pragma unroll
-      for (int hh = 0; hh < NH; ++hh) {
-        const int r = 32 * t + li;
-        const uint8_t* rp = &k_lds[kb][r * D];
-        v8i ka = lds_read32(rp + 16 * ((4 * hh + g) ^ swz_k<D>(r)), rp + 16 * ((4 * hh + 2 + g) ^ swz_k<D>(r)));
-        if constexpr (QK_MX) {
-          int ke;
-          if constexpr (D == 128) ke = (ke_lds[kb][32 * t + kperm(li)] >> (8 * (2 * hh + g))) & 0xff;
-          else ke = reinterpret_cast<const uint8_t*>(&ke_lds[kb][0])[2 * (32 * t + kperm(li)) + g];
-          s[t] = mfma32<true>(ka, qop[hh], s[t], ke, qe[hh]);
-        } else {
-          s[t] = mfma32<false>(ka, qop[hh], s[t], 0, 0);
-        }
-      }
+      for (int c = 0; c < D / 64; ++c) g2l4(va + 64 * c, 4 * lane, vmb + offsetof(VMeta<D>, valpha) + 256 * c);
     }
   };
 
-  // prologue: tile 0 complete, K codes of tile 1
+  // qm correction folded into the scores: the MFMA accumulator of a key starts
+  // at bias / C (C = the score scale of the lane's query and the key's group),
+  // so acc * C = dot * C + bias.  Each wave rescales its bias row of the tile
+  // into two rows of its own LDS area, one per 16-query half of the wave (the
+  // halves can straddle an fp8_block Q scale of 16 rows); lane k handles key k.
+  float qCh0 = qC, qCh1 = qC;
+  if constexpr (HAS_BIAS && !QK_MX) {
+    qCh0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qC), 0));
+    qCh1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qC), 16));
+  }
+  const float inv_qC0 = 1.0f / qCh0, inv_qC1 = 1.0f / qCh1;
+  // Ct_next: the score scale C of the lane's query for the two 16-key groups
+  // (t = 0, 1) of the lane in the next tile, read with the K-side metadata
+  float Ct_next[2] = {qC, qC};
+  // bias_fetch reads the K-side metadata of the tile in slot sl (and sets
+  // Ct_next); bias_store turns it into the wave's two binit rows.  Split so the
+  // LDS reads issue first in a step and the rows are written once they land.
+  struct BiasIn {
+    float b, ks;  // bias of key `lane` (log2 units), fp8_block scale of its group
+  };
+  auto bias_fetch = [&](int sl) -> BiasIn {
+    BiasIn x{0.0f, 1.0f};
+    if constexpr (!QK_MX) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) Ct_next[t] = qC * kmeta[sl].ksc[16 * (2 * t + g)];
+    }
+    if constexpr (HAS_BIAS) {
+      x.b = kmeta[sl].bias[wave][lane];
+      if constexpr (!QK_MX) x.ks = kmeta[sl].ksc[lane];
+    }
+    return x;
+  };
+  auto bias_store = [&](const BiasIn& x) {
+    if constexpr (HAS_BIAS) {
+      float r = 1.0f;
+      if constexpr (!QK_MX) r = __builtin_amdgcn_rcpf(x.ks);
+      binit[wave][0][lane] = x.b * (inv_qC0 * r);
+      binit[wave][1][lane] = x.b * (inv_qC1 * r);
+    }
+  };
+  // S^T = K Q^T (+ bias / C) of the K tile in slot kb
+  // per-lane byte offsets of the MFMA operand reads within a K / V^T slot:
+  // the XOR swizzle of row 32 * t + li (K) or 32 * db + li (V^T) depends on li
+  // only, so the block index becomes an immediate offset of the LDS read.
+  uint32_t krd[NH][2], vrd[2];
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) krd[hh][h2] = li * D + 16 * ((4 * hh + 2 * h2 + g) ^ swz_k<D>(li));
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) vrd[h2] = li * kTN + 16 * ((2 * h2 + g) ^ swz_v(li));
+
+  // ---- S^T = K Q^T (+ bias / C) on the matrix cores ------------------------------
+  constexpr int NQK = 2 * NH;  // QK MFMAs per tile: i = NH * t + hh (32-key block t, 64-wide half hh of D)
+  // accumulator init of score block t: bias / C of the lane's query half (zero without bias)
+  auto qk_init = [&](v16f& s, int t) {
+    if constexpr (HAS_BIAS) {
+      const float4* bp = reinterpret_cast<const float4*>(&binit[wave][li >> 4][32 * t + 16 * g]);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 bb = bp[q4];
+        s[4 * q4 + 0] = bb.x; s[4 * q4 + 1] = bb.y; s[4 * q4 + 2] = bb.z; s[4 * q4 + 3] = bb.w;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+    }
+  };
+  // K operand of QK MFMA i of the tile in K slot kb
+  auto qk_read = [&](int kb, int i) -> v8i {
+    const uint8_t* rp = &k_lds[kb][32 * (i / NH) * D];
+    return lds_read32(rp + krd[i % NH][0], rp + krd[i % NH][1]);
+  };
+  // E8M0 of the K rows of QK MFMA i (MX K; unused otherwise)
+  auto qk_scale = [&](int kb, int i) -> int {
+    if constexpr (QK_MX) {
+      const int t = i / NH, hh = i % NH;
+      if constexpr (D == 128) return (kmeta[kb].ke[32 * t + kperm(li)] >> (8 * (2 * hh + g))) & 0xff;
+      else return reinterpret_cast<const uint8_t*>(&kmeta[kb].ke[0])[2 * (32 * t + kperm(li)) + g];
+    } else {
+      return 127;
+    }
+  };
+  auto qk_mfma = [&](int i, const v8i& ka, const v16f& c_in, int ke) -> v16f {
+    const int hh = i % NH;
+    if constexpr (QK_MX) return mfma32<true>(ka, qop[hh], c_in, ke, qe[hh]);
+    else return mfma32<false>(ka, qop[hh], c_in, 0, 0);
+  };
+  // ---- O^T += V^T P^T (E8M0 scales: MX V columns, MX P; 127 = 1 otherwise) ----------
+  auto pv_read = [&](int vs, int db) -> v8i {
+    const uint8_t* vp = &v_lds[vs][32 * db * kTN];
+    return lds_read32(vp + vrd[0], vp + vrd[1]);
+  };
+  // E8M0 of V^T row 32 db + li (127 unless V is MX)
+  auto pv_scale = [&](int vs, int db) -> int { return reinterpret_cast<const uint8_t*>(&vmeta[vs].ve[0])[32 * db + li]; };
+  auto pv_mfma = [&](int db, const v8i& va, const v8i& pcodes, int pe_, int ve) {
+    acc[db] = mfma32<true>(va, pcodes, acc[db], ve, pe_);
+  };
+
+  // prologue: tiles 0 and 1 complete, K codes of tile 2.  V slot 3 stands for
+  // tile -1: zero codes with unit scales, so the PV that the first step issues
+  // for the previous tile adds exactly zero.
   load_k(0, 0);
   load_v(0, 0);
-  load_k(nt > 1 ? 1 : 0, 1);
-  lds_publish();
-  v16f s_a[2], s_b[2];
-  scores(0, s_a);
-  __syncthreads();  // every wave has read K tile 0 before it is overwritten
+  load_k(nt > 1 ? 1 : nt - 1, 1);
+  load_v(nt > 1 ? 1 : nt - 1, 1);
+  load_k(nt > 2 ? 2 : nt - 1, 2);
+  {
+    uint4* z = reinterpret_cast<uint4*>(&v_lds[3][0]);
+    for (int i = tid; i < D * kTN / 16; i += kThreads) z[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < kTN) vmeta[3].ve[tid] = 0x7f7f7f7fu;
+  }
+  lds_publish<0>();
+  v16f sc[2];
+  bias_store(bias_fetch(0));
+  qk_init(sc[0], 0);
+  qk_init(sc[1], 1);
+#pragma unroll
+  for (int i = 0; i < NQK; ++i) sc[i / NH] = qk_mfma(i, qk_read(0, i), sc[i / NH], qk_scale(0, i));
+  __syncthreads();  // every wave has read K tile 0 and its bias rows before they are overwritten
 
-  // one K/V tile: softmax of s_cur (tile it) while the scores of tile it+1
-  // are computed into s_nxt
-  auto step = [&](const int it, v16f (&s_cur)[2], v16f (&s_nxt)[2]) __attribute__((always_inline)) {
-    const int cur = it & 1;
+  // One K/V tile per step.  Step it turns the scores of tile it (in sc) into P
+  // codes in four chunks of 8 keys per lane.  The matrix work rides along, one
+  // or two MFMAs per chunk, independent of the chunk's VALU work: the PV of
+  // tile it-1 (its codes kept in registers, its V^T in a four-slot ring) and
+  // the QK MFMAs of tile it+1, written into the score block that chunks 0-1
+  // have already consumed (block 0) or after chunk 3 (block 1).  The
+  // accumulator rescale for tile it closes the step, so the PV of tile it in
+  // the next step accumulates into it directly.
+  int slot = 0;       // K slot of tile it (tile i in slot i % 3); V^T slot: tile i in slot i % 4
+  v8i pop_prev;       // P codes of tile it-1 (zero codes before the first tile)
+  int pe_prev = 127;  // their E8M0 scale (MX P)
+#pragma unroll
+  for (int q = 0; q < 8; ++q) pop_prev[q] = 0;
+  // MASKED: the tile holds keys >= S (only the last tile, when S % 64 != 0);
+  // the body is instantiated with and without the masking so the common tiles
+  // carry no merge of masked and unmasked scores
+  auto step = [&](const int it, auto masked_tag) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    const int cur = slot, nxt = slot == 2 ? 0 : slot + 1;
+    const int vprev = (it - 1) & 3, vcur = it & 3;
     const int key0 = it * kTN;
-    // global -> LDS prefetch: K of tile it+2 into the buffer of tile it (read
-    // before the last barrier), V and metadata of tile it+1 (clamped: the last
-    // iterations reload the last tile into buffers nobody reads any more)
-    load_k(it + 2 < nt ? it + 2 : nt - 1, cur);
-    load_v(it + 1 < nt ? it + 1 : nt - 1, 1 - cur);
-    // scores of the next tile run on the matrix cores during this softmax
-    if (it + 1 < nt) scores(1 - cur, s_nxt);
-    const KMeta& km = kmeta[cur];
+    // global -> LDS prefetch: K of tile it+3 into the slot of tile it (read in
+    // the previous step), V^T and metadata of tile it+2 into the slot of tile
+    // it-2 (clamped: the last iterations reload the last tile into slots
+    // nobody reads any more)
+    load_k(it + 3 < nt ? it + 3 : nt - 1, cur);
+    load_v(it + 2 < nt ? it + 2 : nt - 1, (it + 2) & 3);
 
-    // ---- scores in log2 units: u = dot * C (+ qm correction), masked ------------
-    float u[32];
+    // ---- scores: sv = dot + bias / C; the log2-unit score is u = sv * C ----------
+    const float Ct[2] = {Ct_next[0], Ct_next[1]};
+    // LDS reads first, in the order they are consumed, so each wait covers
+    // only what it needs: metadata of tile it+1 (bias rows, Ct_next), the E8M0
+    // scales of this step's MFMAs, the V block scale, the first operands
+    const BiasIn bn = bias_fetch(nxt);
+    int ve_p[NDB], ke_n[NQK];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      float C = qC;
-      if constexpr (!QK_MX) C *= km.ksc[2 * t + g];
-      if constexpr (HAS_BIAS) {
-        const float4* bp = reinterpret_cast<const float4*>(&km.bias[wave][32 * t + 16 * g]);
+    for (int db = 0; db < NDB; ++db) ve_p[db] = pv_scale(vprev, db);
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          float4 bb = bp[q4];
-          u[16 * t + 4 * q4 + 0] = fmaf(s_cur[t][4 * q4 + 0], C, bb.x);
-          u[16 * t + 4 * q4 + 1] = fmaf(s_cur[t][4 * q4 + 1], C, bb.y);
-          u[16 * t + 4 * q4 + 2] = fmaf(s_cur[t][4 * q4 + 2], C, bb.z);
-          u[16 * t + 4 * q4 + 3] = fmaf(s_cur[t][4 * q4 + 3], C, bb.w);
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) u[16 * t + r] = s_cur[t][r] * C;
-      }
-    }
-    if (key0 + kTN > S) {
+    for (int i = 0; i < NQK; ++i) ke_n[i] = qk_scale(nxt, i);
+    const float vsc = vmeta[vcur].vsc[0];
+    v8i va[2], ka[2];
+    va[0] = pv_read(vprev, 0);
+    ka[0] = qk_read(nxt, 0);
+    // sv(j) is the accumulator register of key j (16 * t + r), used in place
+#define sv(j) sc[(j) >> 4][(j) & 15]
+    if constexpr (MASKED) {
 #pragma unroll
       for (int j = 0; j < 32; ++j)
-        if (key0 + 32 * (j >> 4) + 16 * g + (j & 15) >= S) u[j] = -INFINITY;
+        if (key0 + 32 * (j >> 4) + 16 * g + (j & 15) >= S) sv(j) = -INFINITY;
     }
-    float bmax = u[0];
+    float bmax;
+    {
+      float m2v[2];
 #pragma unroll
-    for (int j = 1; j < 32; ++j) bmax = fmaxf(bmax, u[j]);
-    bmax = xor32_max(bmax);
+      for (int t = 0; t < 2; ++t) {
+        // 16 values, 8 instructions, depth 3
+        const float a0 = hmax3(sc[t][0], sc[t][1], sc[t][2]);
+        const float a1 = hmax3(sc[t][3], sc[t][4], sc[t][5]);
+        const float a2 = hmax3(sc[t][6], sc[t][7], sc[t][8]);
+        const float a3 = hmax3(sc[t][9], sc[t][10], sc[t][11]);
+        const float a4 = hmax3(sc[t][12], sc[t][13], sc[t][14]);
+        const float b0 = hmax3(a0, a1, sc[t][15]);
+        m2v[t] = hmax3(b0, a2, hmax(a3, a4)) * Ct[t];   // C > 0
+      }
+      bmax = xor32_max(hmax(m2v[0], m2v[1]));
+    }
 
     // ---- row max, P in quantised units, row sum ----------------------------------
     float alpha, m_new;
-    float pq[32];
     float s_lp;          // P_deq = code * s_lp
     int pe = 127;        // E8M0 of the MX P scale
     float sig_p = 1.0f;  // fp32 P scale carried by the accumulator (dynamic)
     float psum = 0.0f;   // this lane's sum of the pre-quant p
+    v8i pop;             // P codes of tile it
     if constexpr (!BLASST) {
       float T;
       if constexpr (HAS_EST && P_MODE == 2) {
-        if (dyn_est) {
-          const bool lzero = (l == 0.0f) && (__shfl_xor(l, 32, 64) == 0.0f);
-          const float ms = fmaxf(max_seen, bmax);
-          const bool under = (bmax - m2) > 16.0f;
-          const bool over = (m2 - ms) > 32.0f;
-          const float down = lzero ? ms : fmaxf(ms + 32.0f, m2 - 80.0f * kLog2e);
-          const bool adjust = under || over;
-          m_new = adjust ? (under ? bmax : down) : m2;
-          alpha = adjust ? (lzero ? 0.0f : fast_exp2(m2 - m_new)) : 1.0f;
-          max_seen = ms;
-        } else {
-          m_new = est2;
-          alpha = 1.0f;
-        }
+        // branch-free: without dyn_est, m2 stays at the estimate (adjust is false)
+        const bool lzero = xor32_add(l) == 0.0f;  // l >= 0 in both halves
+        const float ms = hmax(max_seen, bmax);
+        const bool under = (bmax - m2) > 16.0f;
+        const bool over = (m2 - ms) > 32.0f;
+        const float down = lzero ? ms : fmaxf(ms + 32.0f, m2 - 80.0f * kLog2e);
+        const bool adjust = dyn_est && (under || over);
+        m_new = adjust ? (under ? bmax : down) : m2;
+        alpha = adjust ? (lzero ? 0.0f : fast_exp2(m2 - m_new)) : 1.0f;
+        max_seen = dyn_est ? ms : max_seen;
       } else if constexpr (HAS_EST) {
         m_new = est2;
         alpha = 1.0f;
       } else {
-        m_new = fmaxf(m2, bmax);
+        m_new = hmax(m2, bmax);
         alpha = fast_exp2(m2 - m_new);
       }
       if constexpr (P_MODE == 0) {
@@ -549,22 +733,91 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
         T = (floored ? m_new + kLog2DynFloor : bmax) - kLog2Fp8Max;
         sig_p = s_lp;
       }
+      // p may exceed 448 only against an estimated or offset row max: satfinite cast
+      const bool clamp = P_MODE == 0 && (HAS_EST || a.p_max_offset > 8);
+      float ps4[4];
+      v16f bi1;
 #pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        pq[j] = fast_exp2(u[j] - T);
-        psum += pq[j];
-      }
-      if constexpr (P_MODE == 0) {
-        if (HAS_EST || a.p_max_offset > 8) {  // p may exceed 448: satfinite cast
-#pragma unroll
-          for (int j = 0; j < 32; ++j) pq[j] = fminf(pq[j], kFp8Max);
+      for (int c = 0; c < 4; ++c) {
+        __builtin_amdgcn_sched_barrier(0);
+        float Tc = T;
+        pin(Tc);
+        // matrix work of chunk c: PV block c of tile it-1, QK MFMAs of block 0 of
+        // tile it+1 (its scores were consumed by chunks 0-1)
+        if (c < NDB) {
+          v8i vac = va[c & 1];
+          pin(vac);
+          if (c + 1 < NDB) va[(c + 1) & 1] = pv_read(vprev, c + 1);
+          pv_mfma(c, vac, pop_prev, pe_prev, ve_p[c]);
         }
+        if (c >= 2 && c - 2 < NH) {
+          v8i kac = ka[(c - 2) & 1];
+          pin(kac);
+          sc[0] = qk_mfma(c - 2, kac, sc[0], ke_n[c - 2]);
+          if (c < NQK) ka[c & 1] = qk_read(nxt, c);
+        }
+        if (c == 0 && NQK > 1) ka[1] = qk_read(nxt, 1);
+        if (c == 0) bias_store(bn);  // bias rows of tile it+1 -> this wave's binit rows
+        if (c == 2) qk_init(bi1, 1);  // accumulator init of score block 1 (bias of tile it+1)
+        // VALU work of chunk c: keys 8c .. 8c+7 of the lane
+        float pq[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int j = 8 * c + jj;
+          pq[jj] = fast_exp2(fmaf(sv(j), Ct[j >> 4], -Tc));
+          ps4[j & 3] = j < 4 ? pq[jj] : ps4[j & 3] + pq[jj];
+        }
+        if constexpr (P_MODE == 0) {
+          if (clamp) {
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) pq[jj] = fminf(pq[jj], kFp8Max);
+          }
+        }
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          // both 16-bit halves are written: the "old" operand only names a register
+          // (pq[4 h2], dead after this instruction), so no zeroing is needed
+          int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2], pq[4 * h2 + 1], __float_as_int(pq[4 * h2]), false);
+          pop[2 * c + h2] = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2 + 2], pq[4 * h2 + 3], wd, true);
+        }
+        // score block 0 is consumed: it receives the bias of tile it+1
+        if (c == 1) qk_init(sc[0], 0);
+        use(pop[2 * c]);
+        use(pop[2 * c + 1]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) use(ps4[k]);
+        if (c < NDB) use(acc[c]);
+        if (c >= 2 && c - 2 < NH) use(sc[0]);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      // score block 1 is consumed: QK MFMAs of tile it+1 from the bias init
+      sc[1] = qk_mfma(NH, ka[NH & 1], bi1, ke_n[NH]);
+#pragma unroll
+      for (int i = NH + 1; i < NQK; ++i) sc[1] = qk_mfma(i, ka[i & 1], sc[1], ke_n[i]);
+      psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
       psum *= s_lp;  // sum of the pre-quant p
     } else {
       // BLASST: explicit p (fills replace skipped rows), then the P scale of the
       // resulting row, exactly in the reference order.
-      const float mij = fmaxf(m2, bmax);
+      float u[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) u[j] = sv(j) * Ct[j >> 4];
+      // sc is free: the matrix work of the step runs under the fill logic
+      bias_store(bn);
+      qk_init(sc[0], 0);
+      qk_init(sc[1], 1);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        if (db + 1 < NDB) va[(db + 1) & 1] = pv_read(vprev, db + 1);
+        pv_mfma(db, va[db & 1], pop_prev, pe_prev, ve_p[db]);
+      }
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) {
+        if (i + 1 < NQK) ka[(i + 1) & 1] = qk_read(nxt, i + 1);
+        sc[i / NH] = qk_mfma(i, ka[i & 1], sc[i / NH], ke_n[i]);
+      }
+      float pq[32];
+      const float mij = hmax(m2, bmax);
       const bool skip = qvalid && (bmax - mij) < a.log2_lam;
       alpha = skip ? 1.0f : fast_exp2(m2 - mij);
       m_new = skip ? m2 : mij;
@@ -580,8 +833,12 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
           for (int j = 0; j < 32; ++j) pq[j] = fillv[j];
         }
       }
+      {
+        float ps4[4] = {pq[0], pq[1], pq[2], pq[3]};
 #pragma unroll
-      for (int j = 0; j < 32; ++j) psum += pq[j];
+        for (int j = 4; j < 32; ++j) ps4[j & 3] += pq[j];
+        psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+      }
       s_lp = 1.0f;
       float qmul = 1.0f;
       if constexpr (P_MODE == 1) {
@@ -605,41 +862,17 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
       }
 #pragma unroll
       for (int j = 0; j < 32; ++j) pq[j] = fminf(pq[j] * qmul, kFp8Max);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * q], pq[4 * q + 1], __float_as_int(pq[4 * q]), false);
+        pop[q] = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * q + 2], pq[4 * q + 3], wd, true);
+      }
     }
     l = l * alpha + psum;
-
-    v8i pop;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * q], pq[4 * q + 1], 0, false);
-      wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * q + 2], pq[4 * q + 3], wd, true);
-      pop[q] = wd;
-    }
-
-    // ---- accumulator rescale (alpha, dynamic P scale, fp8_block V scale) ---------
-    const VMeta<D>& vm = vmeta[cur];
-    float sig_new = sig_p;
-    if (a.v_kind == 1) sig_new *= vm.vsc;
-    const float f = alpha * sigma * __builtin_amdgcn_rcpf(sig_new);
-    sigma = sig_new;
-    if (P_MODE == 2 || __any(f != 1.0f)) {
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[db][r] *= f;
-    }
-
-    // ---- O^T += V^T P^T (E8M0 scales: MX V columns, MX P; 127 = 1 otherwise) -------
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int r = 32 * db + li;
-      const uint8_t* vp = &v_lds[cur][r * kTN];
-      v8i va = lds_read32(vp + 16 * (g ^ swz_v(r)), vp + 16 * ((2 + g) ^ swz_v(r)));
-      const int ve = static_cast<int>((vm.ve[(32 * db + li) >> 2] >> (8 * (li & 3))) & 0xff);
-      acc[db] = mfma32<true>(va, pop, acc[db], ve, pe);
-    }
+#undef sv
 
     // ---- V-smoothing accumulator: c = c * alpha + rowsum(P_deq) (x) alpha_v -------
+    const VMeta<D>& vm = vmeta[vcur];
     if constexpr (VALPHA) {
       float cs = 0.0f;
 #pragma unroll
@@ -657,15 +890,36 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
           cacc[db][r] = fmaf(rs, vm.valpha[d], cacc[db][r] * alpha);
         }
     }
+
+    // ---- accumulator rescale for tile it (alpha, dynamic P scale, fp8_block V
+    // scale): the PV of tile it, issued in the next step, accumulates on top ------
+    float sig_new = sig_p;
+    sig_new *= v_blk ? vsc : 1.0f;
+    const float f = alpha * sigma * __builtin_amdgcn_rcpf(sig_new);
+    sigma = sig_new;
+    if (P_MODE == 2 || __any(f != 1.0f)) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] *= f;
+    }
+    pop_prev = pop;
+    pe_prev = pe;
     m2 = m_new;
 
-    lds_publish();
+    lds_publish<kCopies>();
+    slot = nxt;
   };
-  for (int it = 0; it < nt; ++it) {
-    step(it, s_a, s_b);
+  const int nfull = (S % kTN) ? nt - 1 : nt;
+  for (int it = 0; it < nfull; ++it) step(it, std::false_type{});
+  if (nfull < nt) step(nt - 1, std::true_type{});
+  // PV of the last tile; no copy is left in flight when the workgroup ends
+  {
+    const int vl = (nt - 1) & 3;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) s_a[t] = s_b[t];
+    for (int db = 0; db < NDB; ++db) pv_mfma(db, pv_read(vl, db), pop_prev, pe_prev, pv_scale(vl, db));
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
   // ---- epilogue ---------------------------------------------------------------------
   const float lfull = xor32_add(l);

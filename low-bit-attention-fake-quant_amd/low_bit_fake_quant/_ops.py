@@ -125,20 +125,26 @@ def kmeans(x: torch.Tensor, k: int, iters: int, seed: int):
     return labels, order, inverse
 
 
-def qmk(qm: torch.Tensor, k_s: torch.Tensor, sm_scale: float, *, s_pitch: int, want_bias: bool = True,
-        want_rowmax: bool = True, gather: torch.Tensor | None = None):
-    """bias (B,H,G,s_pitch) = qm.K_s * sm_scale and rowmax (B,H,G) = max_n bias."""
+def qmk(qm: torch.Tensor, k: RowSource, sm_scale: float, *, s_pitch: int, want_bias: bool = True,
+        want_rowmax: bool = True):
+    """bias (B,H,G,s_pitch) = qm.K_s * sm_scale and rowmax (B,H,G) = max_n bias,
+    with K_s the smoothed (and gathered) K described by ``k``: no K_s tensor is
+    materialised when ``k`` subtracts a per-(b,h) column mean."""
     lib = _lib.load()
-    b, s, h, d = k_s.shape
+    x = k.x
+    b, s, h, d = x.shape
     g = qm.shape[1]
-    dev = k_s.device
+    dev = x.device
+    if k.sub_mode not in (_lib.SUB_NONE, _lib.SUB_COLVEC):
+        raise ValueError("qmk: K smoothing is a per-(b,h) column mean")
     bias = None
     if want_bias:
         alloc = torch.zeros if s_pitch > s else torch.empty
         bias = alloc((b, h, g, s_pitch), dtype=torch.float32, device=dev)
     rowmax = torch.empty((b, h, g), dtype=torch.float32, device=dev) if want_rowmax else None
     qm = qm.contiguous().float()
-    _lib.check(lib.lbfq_qmk(qm.data_ptr(), k_s.data_ptr(), _dt(k_s), _lib.ptr(gather), b, s, h, d, g,
+    mean = k.sub if k.sub_mode == _lib.SUB_COLVEC else None
+    _lib.check(lib.lbfq_qmk(qm.data_ptr(), x.data_ptr(), _dt(x), _lib.ptr(k.gather), _lib.ptr(mean), b, s, h, d, g,
                             float(sm_scale), _lib.ptr(bias), int(s_pitch), _lib.ptr(rowmax),
                             _lib.stream_handle(dev)), "lbfq_qmk")
     return bias, rowmax

@@ -187,7 +187,7 @@ def _kmeans_result(src_tensor, km) -> Optional[KMeansReorderResult]:
 # ---------------------------------------------------------------------------
 
 
-def _quant_qk_codes(src: RowSource, cfg: QuantConfig, P: int, *, signs, k_smooth_out=None):
+def _quant_qk_codes(src: RowSource, cfg: QuantConfig, P: int, *, signs):
     """Quantise one of Q/K into head-major codes (B,H,P,D) and the kernel's scales:
     fp8_block -> (B,H,S/block) fp32; mxfp8 -> (B,H,P,D/32) E8M0 bytes."""
     b, s, h, d = src.shape
@@ -202,7 +202,7 @@ def _quant_qk_codes(src: RowSource, cfg: QuantConfig, P: int, *, signs, k_smooth
         scale = torch.empty((b, h, nb), dtype=torch.float32, device=dev)
         rowtile(src, R=blk, hadamard=cfg.qk_hadamard, signs=signs, had_scale=hs, quant_mode=_lib.Q_FP8_BLOCK,
                 codes=codes, codes_layout=_lib.LAYOUT_BHSD, codes_spitch=P, scale=scale,
-                scale_strides=(h * nb, 1, nb, 0), smoothed=k_smooth_out)
+                scale_strides=(h * nb, 1, nb, 0))
     elif cfg.qk_quant == "mxfp8":
         bd = cfg.mxfp8_block_size
         if d % bd != 0:
@@ -212,7 +212,7 @@ def _quant_qk_codes(src: RowSource, cfg: QuantConfig, P: int, *, signs, k_smooth
         scale = torch.zeros((b, h, P, nb), dtype=torch.uint8, device=dev)
         rowtile(src, R=64, hadamard=cfg.qk_hadamard, signs=signs, had_scale=hs, quant_mode=_lib.Q_MX_QK,
                 codes=codes, codes_layout=_lib.LAYOUT_BHSD, codes_spitch=P, scale=scale,
-                scale_strides=(h * P * nb, nb, P * nb, 1), mx_block=bd, smoothed=k_smooth_out, scale_e8m0=True)
+                scale_strides=(h * P * nb, nb, P * nb, 1), mx_block=bd, scale_e8m0=True)
     else:
         raise ValueError(f"unsupported qk_quant: {cfg.qk_quant!r}")
     return codes, scale
@@ -286,8 +286,7 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
     if cfg.qk_hadamard and cfg.qk_hadamard_random_sign:
         signs = qk_signs_device(h, d, cfg.qk_hadamard_seed, prep.q.x.device)
     q_codes, q_scale = _quant_qk_codes(prep.q, cfg, P, signs=signs)
-    k_s = torch.empty_like(prep.k.x) if has_qm else None
-    k_codes, k_scale = _quant_qk_codes(prep.k, cfg, P, signs=signs, k_smooth_out=k_s)
+    k_codes, k_scale = _quant_qk_codes(prep.k, cfg, P, signs=signs)
     v_codes, v_scale, v_kind, v_block = _quant_v_codes(prep.v, cfg, P)
     bias = rowmax = None
     if cfg.rowmax_mode == "qm_k":
@@ -297,7 +296,8 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
         raise ValueError(f"unsupported rowmax_mode: {cfg.rowmax_mode!r}")
     if has_qm:
         # scores are handled in log2 units by the kernel
-        bias, rowmax = qmk(prep.qm, k_s, sm_scale * LOG2E, s_pitch=P, want_rowmax=cfg.rowmax_mode == "qm_k")
+        # K_s = K - mean is formed inside the qm.K_s kernel (never stored)
+        bias, rowmax = qmk(prep.qm, prep.k, sm_scale * LOG2E, s_pitch=P, want_rowmax=cfg.rowmax_mode == "qm_k")
     v_alpha = None
     if prep.v_alpha is not None:
         v_alpha = prep.v_alpha.permute(0, 2, 1, 3).contiguous()

@@ -193,3 +193,24 @@ def test_sdpa_path_with_q_smoothing_and_kmeans(gpu):
     ref = opipe.fake_quant_attention(q, k, v, cfg)
     c, m = cosine(out, ref), max_abs(out, ref)
     assert c >= COS_MIN and m <= MAXABS, f"cos={c:.6f} maxabs={m:.3e}"
+
+
+@pytest.mark.parametrize("name", ["c1_elementwise_online_konly", "c2_dynamic_qmk_full_kmeans", "c3_mxfp8_everything",
+                                  "mx_qmk_fixed_fp8blockV", "fp8blockV_elementwise_vsmooth"])
+def test_attention_is_deterministic(gpu, name):
+    """Two calls on the same inputs give bitwise-identical outputs (the staged
+    global->LDS copies are always complete before a tile's data is read)."""
+    from low_bit_fake_quant import fake_quant_attention
+    cfg = _cfg(**CASES[name])
+    q, k, v = (t.to(gpu) for t in _inputs(n=4096, seed=31, q_clusters=8, v_bias=True))
+    o1 = fake_quant_attention(q, k, v, cfg)
+    o2 = fake_quant_attention(q, k, v, cfg)
+    assert torch.equal(o1, o2)
+
+
+def test_blasst_is_deterministic(gpu):
+    from low_bit_fake_quant import fake_quant_attention
+    cfg = _cfg(qk_quant="fp8_block", fp8_block_size=64, smoothing="full", q_smooth_block_size=256, q_kmeans_k=16,
+               p_quant="dynamic", rowmax_mode="qm_k", blasst_lambda=0.05, blasst_fill="uta16_a1.5")
+    q, k, v = (t.to(gpu) for t in _inputs(n=4096, seed=32, field=(4, 32, 32)))
+    assert torch.equal(fake_quant_attention(q, k, v, cfg), fake_quant_attention(q, k, v, cfg))

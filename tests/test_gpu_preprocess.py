@@ -77,3 +77,34 @@ def test_kmeans_reorder_bit_exact(gpu, k_clusters, iters):
     assert torch.equal(r.tensor_reordered.cpu(), ref["tensor_reordered"])
     y = cpu_randn(1, 1024, 2, 128, seed=8)
     assert torch.equal(apply_kv_permutation(y.to(gpu), r.order).cpu(), okm.apply_kv_permutation(y, ref["order"]))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("gathered", [False, True])
+def test_qmk_table_and_rowmax(gpu, d, gathered):
+    """qm . K_s table (K_s formed in-kernel from K and its column mean, through an
+    optional row gather) against float64 on the CPU; rowmax is the table's row max."""
+    from low_bit_fake_quant import _lib
+    from low_bit_fake_quant._ops import RowSource, qmk
+    s, h, g = 1000, 3, 4                      # ragged S: padding columns of the table stay zero
+    k = cpu_randn(1, s, h, d, seed=21) * 3 + 1.5
+    qm = cpu_randn(1, g, h, d, seed=22, dtype=torch.float32)
+    mean = opre.k_mean(k)                     # (B,H,D) fp32, the smoothing mean
+    gen = torch.Generator().manual_seed(23)
+    order = torch.stack([torch.randperm(s, generator=gen) for _ in range(h)]).to(torch.int32) if gathered else None
+    src = RowSource(k.to(gpu), gather=order.to(gpu) if gathered else None, sub_mode=_lib.SUB_COLVEC,
+                    sub=mean.to(gpu))
+    scale = 0.127
+    pitch = 1024
+    bias, rowmax = qmk(qm.to(gpu), src, scale, s_pitch=pitch)
+    bias, rowmax = bias.cpu(), rowmax.cpu()
+    kk = k.permute(0, 2, 1, 3)                                         # (B,H,S,D)
+    if gathered:
+        kk = torch.stack([kk[0, i, order[i].long()] for i in range(h)]).unsqueeze(0)
+    ks = (kk.float() - mean[:, :, None, :]).to(torch.bfloat16).double()   # the quantiser's rounding
+    ref = torch.einsum("bghd,bhnd->bhgn", qm.double(), ks) * scale
+    mag = torch.einsum("bghd,bhnd->bhgn", qm.double().abs(), ks.abs()) * scale
+    got = bias[..., :s].double()
+    assert ((got - ref).abs() <= 1e-6 * mag + 1e-30).all()
+    assert torch.count_nonzero(bias[..., s:]) == 0
+    assert torch.equal(rowmax, bias[..., :s].amax(-1))
