@@ -221,127 +221,114 @@ __device__ __forceinline__ float xor32_add(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// ---- BLASST fill values (attention_triton.py:231-324) in the lane layout -----
-// u: scores in log2 units (-inf where masked); p units include the elementwise
-// p_max_offset ("off") as in the reference.
-template <int BS>
-__device__ __forceinline__ void uta_small(const float (&u)[32], float m_new, float off, float fa, int g,
-                                          int key0, int S, float (&fillv)[32]) {
-  const float mnat = m_new / kLog2e;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-#pragma unroll
-    for (int b0 = 0; b0 < 16; b0 += BS) {
-      float bs = 0.0f, bm = -INFINITY, bc = 0.0f;
-#pragma unroll
-      for (int r = b0; r < b0 + BS; ++r) {
-        float x = u[16 * t + r];
-        if (x != -INFINITY) { bs += x / kLog2e; bm = fmaxf(bm, x); bc += 1.0f; }
-      }
-      float sbc = fmaxf(bc, 1.0f);
-      float bmean = bs / sbc;
-      float bound = sbc * fast_exp2(bm - m_new + off);
-      float mass = fminf(fa * sbc * fast_exp2((bmean - mnat) * kLog2e + off), bound);
-      float val = mass / sbc;
-#pragma unroll
-      for (int r = b0; r < b0 + BS; ++r) fillv[16 * t + r] = (key0 + 32 * t + 16 * g + r) < S ? val : 0.0f;
-    }
-  }
-}
+// ---- BLASST fill values (attention_triton.py:229-324) in the lane layout -----
+// A skipped row keeps no exact p; its valid keys get a fill, in p units (which
+// include the elementwise p_max_offset "off", as in the reference).  Scores u
+// are in log2 units (-inf where masked), so the reference's natural-log
+// statistics become: (mean_nat - m_nat) * log2e = mean(u) - m and
+// var_nat * log2e = var(u) * ln2.  Sums run over the lane's 32 keys, then over
+// the lane pair (l, l ^ 32) that holds the rest of the 64-key row.  All of it
+// is select-based (no divergent branches); divides by counts go through a
+// reciprocal, so fills agree with the reference to float rounding.  Each
+// function writes fp[j] (0 on masked keys) and returns the row's largest fill.
+constexpr float kLn2 = 0.6931471805599453f;
 
+__device__ __forceinline__ float valid_or(float u, float other) { return u != -INFINITY ? u : other; }
+
+// UTA bins of BS keys (attention_triton.py:292-323): per bin, from its count,
+// mean and max, fill = min(fa * cnt * 2^(mean-m+off), cnt * 2^(max-m+off)) / cnt.
+// BS <= 16: a bin is a run of BS consecutive keys of the lane; 32: one 16-key
+// run of each lane of the pair; 64: both runs of both.
 template <int BS>
-__device__ __forceinline__ void uta_large(const float (&u)[32], float m_new, float off, float fa, int g,
-                                          int key0, int S, float (&fillv)[32]) {
-  const float mnat = m_new / kLog2e;
-  float bs[2] = {0.0f, 0.0f}, bm[2] = {-INFINITY, -INFINITY}, bc[2] = {0.0f, 0.0f};
+__device__ __forceinline__ float uta_fill(const float (&u)[32], float m_new, float off, float fa, float (&fp)[32]) {
+  constexpr int RUN = BS <= 16 ? BS : 16;  // lane-local keys per run
+  constexpr int NR = 32 / RUN;            // runs of the lane
+  float s[NR], mx[NR], c[NR];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int b = 0; b < NR; ++b) {
+    s[b] = 0.0f; mx[b] = -INFINITY; c[b] = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float x = u[16 * t + r];
-      if (x != -INFINITY) { bs[t] += x / kLog2e; bm[t] = fmaxf(bm[t], x); bc[t] += 1.0f; }
+    for (int r = 0; r < RUN; ++r) {
+      const float x = u[RUN * b + r];
+      s[b] += valid_or(x, 0.0f);
+      mx[b] = hmax(mx[b], x);
+      c[b] += x != -INFINITY ? 1.0f : 0.0f;
     }
-    bs[t] = xor32_add(bs[t]);
-    bm[t] = xor32_max(bm[t]);
-    bc[t] = xor32_add(bc[t]);
+    if constexpr (BS >= 32) {
+      s[b] = xor32_add(s[b]);
+      mx[b] = xor32_max(mx[b]);
+      c[b] = xor32_add(c[b]);
+    }
   }
-  if (BS == 64) {
-    bs[0] += bs[1]; bm[0] = fmaxf(bm[0], bm[1]); bc[0] += bc[1];
-    bs[1] = bs[0]; bm[1] = bm[0]; bc[1] = bc[0];
+  if constexpr (BS == 64) {
+    s[0] += s[1]; mx[0] = hmax(mx[0], mx[1]); c[0] += c[1];
+    s[1] = s[0]; mx[1] = mx[0]; c[1] = c[0];
   }
+  float fmx = 0.0f;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    float sbc = fmaxf(bc[t], 1.0f);
-    float bmean = bs[t] / sbc;
-    float bound = sbc * fast_exp2(bm[t] - m_new + off);
-    float mass = fminf(fa * sbc * fast_exp2((bmean - mnat) * kLog2e + off), bound);
-    float val = mass / sbc;
+  for (int b = 0; b < NR; ++b) {
+    const float sc = fmaxf(c[b], 1.0f), rc = __builtin_amdgcn_rcpf(sc);
+    const float f = fminf(fa * sc * fast_exp2(s[b] * rc - m_new + off), sc * fast_exp2(mx[b] - m_new + off)) * rc;
+    fmx = fmaxf(fmx, f);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) fillv[16 * t + r] = (key0 + 32 * t + 16 * g + r) < S ? val : 0.0f;
+    for (int r = 0; r < RUN; ++r) fp[RUN * b + r] = u[RUN * b + r] != -INFINITY ? f : 0.0f;
   }
+  return xor32_max(fmx);
 }
 
 template <int P_MODE>
-__device__ __forceinline__ void blasst_fill_values(const KArgs& a, const float (&u)[32], float m_new, float bmax,
-                                                   float off, int g, int key0, float (&fillv)[32]) {
-  const int S = a.S;
+__device__ __forceinline__ float blasst_fill(const KArgs& a, const float (&u)[32], float m_new, float bmax, float off,
+                                             int key0, float (&fp)[32]) {
   const int fk = a.fill_kind;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) fillv[j] = 0.0f;
-  if (fk == FILL_ZERO) return;
   const float fa = a.fill_alpha;
   if (fk == FILL_UTA) {
     switch (kTN / a.uta_bins) {
-      case 1: uta_small<1>(u, m_new, off, fa, g, key0, S, fillv); break;
-      case 2: uta_small<2>(u, m_new, off, fa, g, key0, S, fillv); break;
-      case 4: uta_small<4>(u, m_new, off, fa, g, key0, S, fillv); break;
-      case 8: uta_small<8>(u, m_new, off, fa, g, key0, S, fillv); break;
-      case 16: uta_small<16>(u, m_new, off, fa, g, key0, S, fillv); break;
-      case 32: uta_large<32>(u, m_new, off, fa, g, key0, S, fillv); break;
-      default: uta_large<64>(u, m_new, off, fa, g, key0, S, fillv); break;
+      case 1: return uta_fill<1>(u, m_new, off, fa, fp);
+      case 2: return uta_fill<2>(u, m_new, off, fa, fp);
+      case 4: return uta_fill<4>(u, m_new, off, fa, fp);
+      case 8: return uta_fill<8>(u, m_new, off, fa, fp);
+      case 16: return uta_fill<16>(u, m_new, off, fa, fp);
+      case 32: return uta_fill<32>(u, m_new, off, fa, fp);
+      default: return uta_fill<64>(u, m_new, off, fa, fp);
     }
-    return;
   }
-  const float n = static_cast<float>(S - key0 < kTN ? S - key0 : kTN);
-  float ssum = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) ssum += (u[j] == -INFINITY ? 0.0f : u[j] / kLog2e);
-  ssum = xor32_add(ssum);
-  const float mean = ssum / n;
-  const float mnat = m_new / kLog2e;
+  const int nv = a.S - key0 < kTN ? a.S - key0 : kTN;  // valid keys of the row (uniform)
+  const float n = static_cast<float>(nv), rn = 1.0f / n;
   const float max_bound = n * fast_exp2(bmax - m_new + off);
-  float fp = 0.0f;
+  float f = 0.0f;  // FILL_ZERO
   if (fk == FILL_MAX) {
-    fp = max_bound * fa / n;
-  } else if (fk == FILL_MEAN) {
-    fp = fminf(fa * n * fast_exp2((mean - mnat) * kLog2e + off), max_bound) / n;
-  } else if (fk == FILL_LOGN) {
-    float vs = 0.0f;
+    f = max_bound * fa * rn;
+  } else if (fk == FILL_MEAN || fk == FILL_LOGN) {
+    float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      float c = u[j] == -INFINITY ? 0.0f : (u[j] / kLog2e - mean);
-      vs += c * c;
+    for (int j = 0; j < 32; ++j) s += valid_or(u[j], 0.0f);
+    const float mean = xor32_add(s) * rn;  // log2 units
+    if (fk == FILL_MEAN) {
+      f = fminf(fa * n * fast_exp2(mean - m_new + off), max_bound) * rn;
+    } else {
+      float vs = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const float c = valid_or(u[j] - mean, 0.0f);
+        vs = fmaf(c, c, vs);
+      }
+      const float var2 = xor32_add(vs) * rn;  // log2 units squared
+      f = fminf(n * fast_exp2(mean + 0.5f * var2 * kLn2 - m_new + off), max_bound) * rn;
     }
-    vs = xor32_add(vs);
-    float var = vs / n;
-    fp = fminf(n * fast_exp2((mean + 0.5f * var - mnat) * kLog2e + off), max_bound) / n;
   } else if (fk == FILL_SAMPLE8) {
-    // sampled keys rel % 8 == 0 are r in {0, 8} of both 32-key blocks
+    // sampled keys: rel % 8 == 0, i.e. r in {0, 8} of both 16-key runs of the lane
     const float c0 = off - m_new;
-    float sp = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) sp += fast_exp2(u[16 * t] + c0) + fast_exp2(u[16 * t + 8] + c0);
-    sp = xor32_add(sp);
-    float cnt = 0.0f;
-    for (int kk = 0; kk < kTN; kk += 8) cnt += (key0 + kk < S) ? 1.0f : 0.0f;
-    cnt = fmaxf(cnt, 1.0f);
-    fp = fminf(fa * n * sp / cnt, max_bound) / n;
-  } else {  // FILL_THR
-    float offs = P_MODE == 0 ? exp2f(static_cast<float>(a.p_max_offset)) : 1.0f;
-    fp = fa * n * a.lam * offs / n;
+    const float sp = xor32_add(fast_exp2(u[0] + c0) + fast_exp2(u[8] + c0) + fast_exp2(u[16] + c0) +
+                               fast_exp2(u[24] + c0));
+    const float cnt = static_cast<float>((nv + 7) / 8);
+    f = fminf(fa * n * sp / cnt, max_bound) * rn;
+  } else if (fk == FILL_THR) {
+    const float offs = P_MODE == 0 ? exp2f(static_cast<float>(a.p_max_offset)) : 1.0f;
+    f = fa * n * a.lam * offs * rn;
   }
 #pragma unroll
-  for (int j = 0; j < 32; ++j) fillv[j] = (key0 + 32 * (j >> 4) + 16 * g + (j & 15)) < S ? fp : 0.0f;
+  for (int j = 0; j < 32; ++j) fp[j] = u[j] != -INFINITY ? f : 0.0f;
+  return f;
 }
 
 template <int D, bool QK_MX, int P_MODE, int RB, bool BLASST, bool VALPHA>
@@ -633,6 +620,9 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
   int slot = 0;       // K slot of tile it (tile i in slot i % 3); V^T slot: tile i in slot i % 4
   v8i pop_prev;       // P codes of tile it-1 (zero codes before the first tile)
   int pe_prev = 127;  // their E8M0 scale (MX P)
+  float fcq[BLASST ? 32 : 1];  // BLASST: fill codes of the lane's keys (current where the row skips)
+#pragma unroll
+  for (int j = 0; j < (BLASST ? 32 : 1); ++j) fcq[j] = 0.0f;
 #pragma unroll
   for (int q = 0; q < 8; ++q) pop_prev[q] = 0;
   // MASKED: the tile holds keys >= S (only the last tile, when S % 64 != 0);
@@ -691,183 +681,143 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
 
     // ---- row max, P in quantised units, row sum ----------------------------------
     float alpha, m_new;
-    float s_lp;          // P_deq = code * s_lp
     int pe = 127;        // E8M0 of the MX P scale
     float sig_p = 1.0f;  // fp32 P scale carried by the accumulator (dynamic)
-    float psum = 0.0f;   // this lane's sum of the pre-quant p
     v8i pop;             // P codes of tile it
-    if constexpr (!BLASST) {
-      float T;
-      if constexpr (HAS_EST && P_MODE == 2) {
-        // branch-free: without dyn_est, m2 stays at the estimate (adjust is false)
-        const bool lzero = xor32_add(l) == 0.0f;  // l >= 0 in both halves
-        const float ms = hmax(max_seen, bmax);
-        const bool under = (bmax - m2) > 16.0f;
-        const bool over = (m2 - ms) > 32.0f;
-        const float down = lzero ? ms : fmaxf(ms + 32.0f, m2 - 80.0f * kLog2e);
-        const bool adjust = dyn_est && (under || over);
-        m_new = adjust ? (under ? bmax : down) : m2;
-        alpha = adjust ? (lzero ? 0.0f : fast_exp2(m2 - m_new)) : 1.0f;
-        max_seen = dyn_est ? ms : max_seen;
-      } else if constexpr (HAS_EST) {
-        m_new = est2;
-        alpha = 1.0f;
-      } else {
-        m_new = hmax(m2, bmax);
-        alpha = fast_exp2(m2 - m_new);
-      }
-      if constexpr (P_MODE == 0) {
-        T = m_new - off;
-        s_lp = 1.0f;
-      } else if constexpr (P_MODE == 1) {
-        const float ra = fmaxf(fast_exp2(bmax - m_new), kAmaxFloor);
-        int e = ceil_log2_exact(ra / kFp8Max);
-        e = e < -127 ? -127 : (e > 127 ? 127 : e);
-        T = m_new + static_cast<float>(e);
-        s_lp = __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
-        pe = e + 127;
-      } else {
-        const float ra = fast_exp2(bmax - m_new);
-        const bool floored = !(ra > 1e-12f);
-        s_lp = (floored ? 1e-12f : ra) * (1.0f / kFp8Max);
-        T = (floored ? m_new + kLog2DynFloor : bmax) - kLog2Fp8Max;
-        sig_p = s_lp;
-      }
-      // p may exceed 448 only against an estimated or offset row max: satfinite cast
-      const bool clamp = P_MODE == 0 && (HAS_EST || a.p_max_offset > 8);
-      float ps4[4];
-      v16f bi1;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        __builtin_amdgcn_sched_barrier(0);
-        float Tc = T;
-        pin(Tc);
-        // matrix work of chunk c: PV block c of tile it-1, QK MFMAs of block 0 of
-        // tile it+1 (its scores were consumed by chunks 0-1)
-        if (c < NDB) {
-          v8i vac = va[c & 1];
-          pin(vac);
-          if (c + 1 < NDB) va[(c + 1) & 1] = pv_read(vprev, c + 1);
-          pv_mfma(c, vac, pop_prev, pe_prev, ve_p[c]);
-        }
-        if (c >= 2 && c - 2 < NH) {
-          v8i kac = ka[(c - 2) & 1];
-          pin(kac);
-          sc[0] = qk_mfma(c - 2, kac, sc[0], ke_n[c - 2]);
-          if (c < NQK) ka[c & 1] = qk_read(nxt, c);
-        }
-        if (c == 0 && NQK > 1) ka[1] = qk_read(nxt, 1);
-        if (c == 0) bias_store(bn);  // bias rows of tile it+1 -> this wave's binit rows
-        if (c == 2) qk_init(bi1, 1);  // accumulator init of score block 1 (bias of tile it+1)
-        // VALU work of chunk c: keys 8c .. 8c+7 of the lane
-        float pq[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int j = 8 * c + jj;
-          pq[jj] = fast_exp2(fmaf(sv(j), Ct[j >> 4], -Tc));
-          ps4[j & 3] = j < 4 ? pq[jj] : ps4[j & 3] + pq[jj];
-        }
-        if constexpr (P_MODE == 0) {
-          if (clamp) {
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) pq[jj] = fminf(pq[jj], kFp8Max);
-          }
-        }
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          // both 16-bit halves are written: the "old" operand only names a register
-          // (pq[4 h2], dead after this instruction), so no zeroing is needed
-          int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2], pq[4 * h2 + 1], __float_as_int(pq[4 * h2]), false);
-          pop[2 * c + h2] = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2 + 2], pq[4 * h2 + 3], wd, true);
-        }
-        // score block 0 is consumed: it receives the bias of tile it+1
-        if (c == 1) qk_init(sc[0], 0);
-        use(pop[2 * c]);
-        use(pop[2 * c + 1]);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) use(ps4[k]);
-        if (c < NDB) use(acc[c]);
-        if (c >= 2 && c - 2 < NH) use(sc[0]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // score block 1 is consumed: QK MFMAs of tile it+1 from the bias init
-      sc[1] = qk_mfma(NH, ka[NH & 1], bi1, ke_n[NH]);
-#pragma unroll
-      for (int i = NH + 1; i < NQK; ++i) sc[1] = qk_mfma(i, ka[i & 1], sc[1], ke_n[i]);
-      psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
-      psum *= s_lp;  // sum of the pre-quant p
-    } else {
-      // BLASST: explicit p (fills replace skipped rows), then the P scale of the
-      // resulting row, exactly in the reference order.
-      float u[32];
-#pragma unroll
-      for (int j = 0; j < 32; ++j) u[j] = sv(j) * Ct[j >> 4];
-      // sc is free: the matrix work of the step runs under the fill logic
-      bias_store(bn);
-      qk_init(sc[0], 0);
-      qk_init(sc[1], 1);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        if (db + 1 < NDB) va[(db + 1) & 1] = pv_read(vprev, db + 1);
-        pv_mfma(db, va[db & 1], pop_prev, pe_prev, ve_p[db]);
-      }
-#pragma unroll
-      for (int i = 0; i < NQK; ++i) {
-        if (i + 1 < NQK) ka[(i + 1) & 1] = qk_read(nxt, i + 1);
-        sc[i / NH] = qk_mfma(i, ka[i & 1], sc[i / NH], ke_n[i]);
-      }
-      float pq[32];
+    bool skip = false;   // BLASST: the row keeps no exact p in this tile
+    if constexpr (BLASST) {
+      // attention_triton.py:164-175 (BLASST takes precedence over the estimate)
       const float mij = hmax(m2, bmax);
-      const bool skip = qvalid && (bmax - mij) < a.log2_lam;
+      skip = qvalid && (bmax - mij) < a.log2_lam;
       alpha = skip ? 1.0f : fast_exp2(m2 - mij);
       m_new = skip ? m2 : mij;
       if (g == 0) { skipped += skip ? 1.0f : 0.0f; total += qvalid ? 1.0f : 0.0f; }
-      const float c0 = off - m_new;
+    } else if constexpr (HAS_EST && P_MODE == 2) {
+      // branch-free: without dyn_est, m2 stays at the estimate (adjust is false)
+      const bool lzero = xor32_add(l) == 0.0f;  // l >= 0 in both halves
+      const float ms = hmax(max_seen, bmax);
+      const bool under = (bmax - m2) > 16.0f;
+      const bool over = (m2 - ms) > 32.0f;
+      const float down = lzero ? ms : fmaxf(ms + 32.0f, m2 - 80.0f * kLog2e);
+      const bool adjust = dyn_est && (under || over);
+      m_new = adjust ? (under ? bmax : down) : m2;
+      alpha = adjust ? (lzero ? 0.0f : fast_exp2(m2 - m_new)) : 1.0f;
+      max_seen = dyn_est ? ms : max_seen;
+    } else if constexpr (HAS_EST) {
+      m_new = est2;
+      alpha = 1.0f;
+    } else {
+      m_new = hmax(m2, bmax);
+      alpha = fast_exp2(m2 - m_new);
+    }
+    // BLASST fills of the skipped rows, in p units, and the largest fill of the row
+    float fp[BLASST ? 32 : 1];
+    float fmax = 0.0f;
+    bool any_skip = false;
+    if constexpr (BLASST) {
+      any_skip = __any(skip);
+      if (any_skip) {
+        float u[32];
 #pragma unroll
-      for (int j = 0; j < 32; ++j) pq[j] = fast_exp2(u[j] + c0);
-      if (__any(skip)) {
-        float fillv[32];
-        blasst_fill_values<P_MODE>(a, u, m_new, bmax, off, g, key0, fillv);
-        if (skip) {
-#pragma unroll
-          for (int j = 0; j < 32; ++j) pq[j] = fillv[j];
-        }
-      }
-      {
-        float ps4[4] = {pq[0], pq[1], pq[2], pq[3]};
-#pragma unroll
-        for (int j = 4; j < 32; ++j) ps4[j & 3] += pq[j];
-        psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
-      }
-      s_lp = 1.0f;
-      float qmul = 1.0f;
-      if constexpr (P_MODE == 1) {
-        float pa = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) pa = fmaxf(pa, pq[j]);
-        pa = fmaxf(xor32_max(pa), kAmaxFloor);
-        int e = ceil_log2_exact(pa / kFp8Max);
-        e = e < -127 ? -127 : (e > 127 ? 127 : e);
-        pe = e + 127;
-        qmul = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
-        s_lp = __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
-      } else if constexpr (P_MODE == 2) {
-        float pa = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) pa = fmaxf(pa, pq[j]);
-        pa = fmaxf(xor32_max(pa), 1e-12f);
-        s_lp = pa / kFp8Max;
-        sig_p = s_lp;
-        qmul = kFp8Max / pa;
-      }
-#pragma unroll
-      for (int j = 0; j < 32; ++j) pq[j] = fminf(pq[j] * qmul, kFp8Max);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * q], pq[4 * q + 1], __float_as_int(pq[4 * q]), false);
-        pop[q] = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * q + 2], pq[4 * q + 3], wd, true);
+        for (int j = 0; j < 32; ++j) u[j] = sv(j) * Ct[j >> 4];
+        fmax = blasst_fill<P_MODE>(a, u, m_new, bmax, off, key0, fp);
       }
     }
+    // P scale of the row (attention_triton.py:330-370): exact rows from the tile
+    // max, skipped rows from their largest fill; T puts exact p in code units
+    float T, s_lp, qmul_f = 1.0f;  // qmul_f: fill (p units) -> code units
+    if constexpr (P_MODE == 0) {
+      T = m_new - off;
+      s_lp = 1.0f;
+    } else if constexpr (P_MODE == 1) {
+      const float ra = fmaxf(skip ? fmax : fast_exp2(bmax - m_new), kAmaxFloor);
+      int e = ceil_log2_exact(ra / kFp8Max);
+      e = e < -127 ? -127 : (e > 127 ? 127 : e);
+      T = m_new + static_cast<float>(e);
+      s_lp = __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+      qmul_f = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+      pe = e + 127;
+    } else {
+      const float ra = skip ? fmax : fast_exp2(bmax - m_new);
+      const bool floored = !(ra > 1e-12f);
+      const float rf = floored ? 1e-12f : ra;
+      s_lp = rf * (1.0f / kFp8Max);
+      T = (floored ? m_new + kLog2DynFloor : bmax) - kLog2Fp8Max;
+      sig_p = s_lp;
+      if constexpr (BLASST) qmul_f = kFp8Max / rf;
+    }
+    if constexpr (BLASST) {
+      if (any_skip) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) fcq[j] = P_MODE == 0 ? fminf(fp[j], kFp8Max) : fp[j] * qmul_f;
+      }
+    }
+    (void)qmul_f;
+    (void)fp;
+    // p may exceed 448 only against an estimated or offset row max: satfinite cast
+    const bool clamp = P_MODE == 0 && (HAS_EST || a.p_max_offset > 8);
+    float ps4[4];
+    v16f bi1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      __builtin_amdgcn_sched_barrier(0);
+      float Tc = T;
+      pin(Tc);
+      // matrix work of chunk c: PV block c of tile it-1, QK MFMAs of block 0 of
+      // tile it+1 (its scores were consumed by chunks 0-1)
+      if (c < NDB) {
+        v8i vac = va[c & 1];
+        pin(vac);
+        if (c + 1 < NDB) va[(c + 1) & 1] = pv_read(vprev, c + 1);
+        pv_mfma(c, vac, pop_prev, pe_prev, ve_p[c]);
+      }
+      if (c >= 2 && c - 2 < NH) {
+        v8i kac = ka[(c - 2) & 1];
+        pin(kac);
+        sc[0] = qk_mfma(c - 2, kac, sc[0], ke_n[c - 2]);
+        if (c < NQK) ka[c & 1] = qk_read(nxt, c);
+      }
+      if (c == 0 && NQK > 1) ka[1] = qk_read(nxt, 1);
+      if (c == 0) bias_store(bn);  // bias rows of tile it+1 -> this wave's binit rows
+      if (c == 2) qk_init(bi1, 1);  // accumulator init of score block 1 (bias of tile it+1)
+      // VALU work of chunk c: keys 8c .. 8c+7 of the lane
+      float pq[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int j = 8 * c + jj;
+        pq[jj] = fast_exp2(fmaf(sv(j), Ct[j >> 4], -Tc));
+        if constexpr (BLASST) pq[jj] = skip ? fcq[j] : pq[jj];  // fill codes of a skipped row
+        ps4[j & 3] = j < 4 ? pq[jj] : ps4[j & 3] + pq[jj];
+      }
+      if constexpr (P_MODE == 0) {
+        if (clamp) {
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) pq[jj] = fminf(pq[jj], kFp8Max);
+        }
+      }
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        // both 16-bit halves are written: the "old" operand only names a register
+        // (pq[4 h2], dead after this instruction), so no zeroing is needed
+        int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2], pq[4 * h2 + 1], __float_as_int(pq[4 * h2]), false);
+        pop[2 * c + h2] = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2 + 2], pq[4 * h2 + 3], wd, true);
+      }
+      // score block 0 is consumed: it receives the bias of tile it+1
+      if (c == 1) qk_init(sc[0], 0);
+      use(pop[2 * c]);
+      use(pop[2 * c + 1]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) use(ps4[k]);
+      if (c < NDB) use(acc[c]);
+      if (c >= 2 && c - 2 < NH) use(sc[0]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // score block 1 is consumed: QK MFMAs of tile it+1 from the bias init
+    sc[1] = qk_mfma(NH, ka[NH & 1], bi1, ke_n[NH]);
+#pragma unroll
+    for (int i = NH + 1; i < NQK; ++i) sc[1] = qk_mfma(i, ka[i & 1], sc[1], ke_n[i]);
+    float psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+    psum *= s_lp;  // sum of the pre-quant p
     l = l * alpha + psum;
 #undef sv
 

@@ -121,7 +121,7 @@ def test_ragged_sequence_length(gpu):
 
 
 @pytest.mark.parametrize("fill", ["zero", "max_a0.25", "mean_a1.5", "logn", "sample8_a1.25", "thr_a0.25",
-                                  "uta16_a1.5", "uta4", "uta2_a1.5", "uta"])
+                                  "uta16_a1.5", "uta4", "uta2_a1.5", "uta", "uta1", "uta8", "uta64_a1.5"])
 def test_blasst_fill_matches_oracle(gpu, fill):
     from low_bit_fake_quant import fake_quant_attention
     cfg = _cfg(qk_quant="fp8_block", fp8_block_size=64, smoothing="full", q_smooth_block_size=256,
@@ -129,6 +129,19 @@ def test_blasst_fill_matches_oracle(gpu, fill):
     q, k, v = _inputs(n=1024, seed=5, field=(4, 16, 16))
     out = fake_quant_attention(q.to(gpu), k.to(gpu), v.to(gpu), cfg).cpu()
     check_parity(out, q, k, v, cfg, fill)
+
+
+@pytest.mark.parametrize("fill", ["mean_a1.5", "logn", "sample8_a1.25", "uta16_a1.5", "uta1"])
+def test_blasst_fill_ragged_matches_oracle(gpu, fill):
+    # S = 1000: the last 64-key tile holds 40 valid keys (masked fill statistics)
+    from low_bit_fake_quant import fake_quant_attention
+    # (fp8_block and Q smoothing need S divisible by their blocks: MX Q/K, K-only
+    # smoothing, online row max)
+    cfg = _cfg(qk_quant="mxfp8", v_quant="fp8_channel", smoothing="k_only", q_kmeans_k=None,
+               p_quant="dynamic", rowmax_mode="online", blasst_lambda=0.05, blasst_fill=fill)
+    q, k, v = _inputs(n=1000, seed=6, field=(4, 10, 25))
+    out = fake_quant_attention(q.to(gpu), k.to(gpu), v.to(gpu), cfg).cpu()
+    check_parity(out, q, k, v, cfg, fill + "/ragged")
 
 
 @pytest.mark.parametrize("p_quant", ["elementwise", "mx", "dynamic"])
