@@ -94,70 +94,59 @@ __device__ __forceinline__ void store8(void* y, int dt, int64_t idx, const float
   }
 }
 
-// Produce the 8 transformed values of (row s_out, cols d0..d0+7) of head
-// (b, h).  Lanes of one row are lanes [g*lpr, g*lpr+lpr) of the wave; the
-// FWHT needs all of them active, so invalid rows still run it on zeros.
-__device__ __forceinline__ void transform8(const RowTileArgs& a, int64_t b, int64_t h, int64_t s_out,
-                                           bool valid, int d0, int lpr, float v[8], bool store_smoothed) {
-  if (valid) {
-    int64_t src = s_out;
-    if (a.gather) src = a.gather[(b * a.H + h) * a.S + s_out];
-    load8(a.x, a.x_dtype, ((b * a.S + src) * a.H + h) * a.D + d0, v);
-    if (a.sub_mode != LBFQ_SUB_NONE) {
-      const float* m;
-      if (a.sub_mode == LBFQ_SUB_COLVEC) m = a.sub + (b * a.H + h) * a.D + d0;
-      else m = a.sub + ((b * (a.S / a.sub_block) + s_out / a.sub_block) * a.H + h) * a.D + d0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = round_to_dtype(v[i] - m[i], a.x_dtype);
-    }
-    if (store_smoothed && a.smoothed && a.smoothed_stage == 0)
-      store8(a.smoothed, a.x_dtype, ((b * a.S + s_out) * a.H + h) * a.D + d0, v);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-  }
-  if (a.hadamard) {
-    if (a.signs) {
-      const int8_t* sg = a.signs + h * a.D + d0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = sg[i] < 0 ? -v[i] : v[i];
-    }
-    // In-lane stages: stride 1, 2, 4.
-#pragma unroll
-    for (int st = 1; st < 8; st <<= 1) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if ((i & st) == 0) {
-          float l = v[i], r = v[i + st];
-          v[i] = l + r;
-          v[i + st] = l - r;
-        }
-      }
-    }
-    // Cross-lane stages: stride 8, 16, ... within the row's lpr lanes.
-    int lane = threadIdx.x & 63;
-    for (int m = 1; m < lpr; m <<= 1) {
-      bool upper = (lane & m) != 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float o = __shfl_xor(v[i], m, 64);
-        v[i] = upper ? (o - v[i]) : (v[i] + o);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = round_to_dtype(v[i] * a.had_scale, a.x_dtype);
-    if (valid && store_smoothed && a.smoothed && a.smoothed_stage == 1)
-      store8(a.smoothed, a.x_dtype, ((b * a.S + s_out) * a.H + h) * a.D + d0, v);
-  }
-}
-
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
   return v;
 }
 
+// Load 8 consecutive elements of dtype DT as fp32 (exact widening).
+template <int DT>
+__device__ __forceinline__ void load8t(const void* x, int64_t idx, float v[8]) {
+  if constexpr (DT == kF32) {
+    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + idx);
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + idx);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xffffu), hi = static_cast<uint16_t>(w[i] >> 16);
+      if constexpr (DT == kBF16) { v[2 * i] = bf16_bits_to_f32(lo); v[2 * i + 1] = bf16_bits_to_f32(hi); }
+      else { v[2 * i] = f16_bits_to_f32(lo); v[2 * i + 1] = f16_bits_to_f32(hi); }
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float round_dt(float v) {
+  if constexpr (DT == kBF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  else if constexpr (DT == kF16) return f16_bits_to_f32(f32_to_f16_bits(v));
+  else return v;
+}
+
+// Encode q / sc (|q / sc| <= 448 after the clamp) with the hardware RNE
+// converter; its agreement with the reference encoder over every code,
+// midpoint, neighbour of a midpoint and the subnormal range is a GPU test.
+__device__ __forceinline__ uint32_t cvt4_e4m3(const float q[4]) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], w, true);
+  return static_cast<uint32_t>(w);
+}
+
+__device__ __forceinline__ float clamp448(float q) { return __builtin_amdgcn_fmed3f(q, -kFp8Max, kFp8Max); }
+
+// Row passes (rows_per_pass rows each) whose data a thread keeps in registers:
+// a batch is loaded with all its loads in flight before any of them is used,
+// and a two-pass tile (block / MX-V scales) of up to kBatch passes is read
+// from memory once.
+constexpr int kBatch = 8;
+
+template <int DT, int QM>
 __global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
+  constexpr bool TWO_PASS = QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_MX_V || QM == LBFQ_Q_CHANNEL_AMAX;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int lpr = static_cast<int>(a.D / 8);       // lanes per row
@@ -172,34 +161,103 @@ __global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
   const int64_t tile = bid % ntile;
   const int64_t b = bid / ntile;
   const int64_t s0 = tile * a.R;
+  const int npass = (a.R + rpp - 1) / rpp;
+  const int tcp = static_cast<int>(a.D) + 4;  // LDS row pitch of the BHDS staging tile (bank spread)
+  const int64_t bh = b * a.H + h;
 
   __shared__ float red[kThreads / 64][128];
   __shared__ float sc_sh[128];
-  extern __shared__ uint8_t tcodes[];  // BHDS staging: R * D bytes
+  extern __shared__ uint8_t tcodes[];  // BHDS staging: R rows of tcp bytes
 
-  const int qm = a.quant_mode;
-  const bool two_pass = (qm == LBFQ_Q_FP8_BLOCK || qm == LBFQ_Q_MX_V || qm == LBFQ_Q_CHANNEL_AMAX);
-  float v[8];
+  const bool resident = TWO_PASS && QM != LBFQ_Q_CHANNEL_AMAX && npass <= kBatch;
 
-  // ---- pass 1: reductions for tile-wide scales -----------------------------
-  float tmax = 0.0f;
-  float cmax[8];
+  float v[kBatch][8];
+  bool ok[kBatch];
+  // load + transform row passes [p0, p0 + kBatch) into v (zeros past the tile)
+  auto load_batch = [&](int p0, bool store_smoothed) {
+    int64_t src[kBatch];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) cmax[i] = 0.0f;
-  if (two_pass) {
-    for (int r0 = 0; r0 < a.R; r0 += rpp) {
-      int r = r0 + wave * rpw + row_in_wave;
-      int64_t s = s0 + r;
-      bool valid = r < a.R && s < a.S;
-      transform8(a, b, h, s, valid, d0, lpr, v, qm == LBFQ_Q_CHANNEL_AMAX);
+    for (int i = 0; i < kBatch; ++i) {
+      const int r = (p0 + i) * rpp + wave * rpw + row_in_wave;
+      const int64_t s = s0 + r;
+      ok[i] = p0 + i < npass && r < a.R && s < a.S;
+      src[i] = ok[i] ? s : s0;  // a safe row for lanes past the tile
+      if (a.gather) src[i] = a.gather[bh * a.S + src[i]];
+    }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float av = valid ? fabsf(v[i]) : 0.0f;
-        tmax = fmaxf(tmax, av);
-        cmax[i] = fmaxf(cmax[i], av);
+    for (int i = 0; i < kBatch; ++i) {
+      if (p0 + i < npass) load8t<DT>(a.x, ((b * a.S + src[i]) * a.H + h) * a.D + d0, v[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (p0 + i >= npass) continue;
+      const int64_t s_out = s0 + (p0 + i) * rpp + wave * rpw + row_in_wave;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[i][k] = ok[i] ? v[i][k] : 0.0f;
+      if (a.sub_mode != LBFQ_SUB_NONE) {
+        const float* m = a.sub_mode == LBFQ_SUB_COLVEC
+                             ? a.sub + bh * a.D + d0
+                             : a.sub + ((b * (a.S / a.sub_block) + (ok[i] ? s_out : s0) / a.sub_block) * a.H + h) * a.D + d0;
+        const float4 m0 = reinterpret_cast<const float4*>(m)[0], m1 = reinterpret_cast<const float4*>(m)[1];
+        const float mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[i][k] = ok[i] ? round_dt<DT>(v[i][k] - mm[k]) : 0.0f;
+      }
+      if (store_smoothed && ok[i] && a.smoothed && a.smoothed_stage == 0)
+        store8(a.smoothed, DT, ((b * a.S + s_out) * a.H + h) * a.D + d0, v[i]);
+      if (a.hadamard) {
+        if (a.signs) {
+          const int8_t* sg = a.signs + h * a.D + d0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) v[i][k] = sg[k] < 0 ? -v[i][k] : v[i][k];
+        }
+#pragma unroll
+        for (int st = 1; st < 8; st <<= 1) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            if ((k & st) == 0) {
+              const float l = v[i][k], rr = v[i][k + st];
+              v[i][k] = l + rr;
+              v[i][k + st] = l - rr;
+            }
+          }
+        }
+        // cross-lane stages: stride 8, 16, ... within the row's lpr lanes
+        for (int m = 1; m < lpr; m <<= 1) {
+          const bool upper = (lane & m) != 0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float o = __shfl_xor(v[i][k], m, 64);
+            v[i][k] = upper ? (o - v[i][k]) : (v[i][k] + o);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[i][k] = round_dt<DT>(v[i][k] * a.had_scale);
+        if (store_smoothed && ok[i] && a.smoothed && a.smoothed_stage == 1)
+          store8(a.smoothed, DT, ((b * a.S + s_out) * a.H + h) * a.D + d0, v[i]);
       }
     }
-    if (qm == LBFQ_Q_FP8_BLOCK) {
+  };
+
+  // ---- pass 1: reductions for tile-wide scales -----------------------------
+  if constexpr (TWO_PASS) {
+    float tmax = 0.0f;
+    float cmax[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cmax[k] = 0.0f;
+    for (int p0 = 0; p0 < npass; p0 += kBatch) {
+      load_batch(p0, resident || QM == LBFQ_Q_CHANNEL_AMAX);
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float av = ok[i] ? fabsf(v[i][k]) : 0.0f;
+          tmax = fmaxf(tmax, av);
+          cmax[k] = fmaxf(cmax[k], av);
+        }
+      }
+    }
+    if constexpr (QM == LBFQ_Q_FP8_BLOCK) {
       tmax = wave_max(tmax);
       if (lane == 0) red[wave][0] = tmax;
       __syncthreads();
@@ -207,7 +265,7 @@ __global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
         float m = red[0][0];
         for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w][0]);
         m = fmaxf(m, kAmaxFloor);
-        float sc = m / kFp8Max;
+        const float sc = m / kFp8Max;
         sc_sh[0] = sc;
         a.scale[b * a.sc_b + tile * a.sc_s + h * a.sc_h] = sc;
       }
@@ -215,91 +273,123 @@ __global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
     } else {
       // per-column max over rows: lanes with equal (lane % lpr) share columns
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        for (int m = lpr; m < 64; m <<= 1) cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], m, 64));
+      for (int k = 0; k < 8; ++k)
+        for (int m = lpr; m < 64; m <<= 1) cmax[k] = fmaxf(cmax[k], __shfl_xor(cmax[k], m, 64));
       if (row_in_wave == 0) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) red[wave][d0 + i] = cmax[i];
+        for (int k = 0; k < 8; ++k) red[wave][d0 + k] = cmax[k];
       }
       __syncthreads();
       if (threadIdx.x < a.D) {
         float m = red[0][threadIdx.x];
         for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w][threadIdx.x]);
-        if (qm == LBFQ_Q_CHANNEL_AMAX) {
-          atomicMax(a.amax_table + (b * a.H + h) * a.D + threadIdx.x, __float_as_uint(m));
+        if constexpr (QM == LBFQ_Q_CHANNEL_AMAX) {
+          atomicMax(a.amax_table + bh * a.D + threadIdx.x, __float_as_uint(m));
         } else {
           m = fmaxf(m, kAmaxFloor);
-          float sc = mx_scale_from_amax(m);
+          const float sc = mx_scale_from_amax(m);
           sc_sh[threadIdx.x] = sc;
-          int64_t si = b * a.sc_b + tile * a.sc_s + h * a.sc_h + threadIdx.x * a.sc_d;
+          const int64_t si = b * a.sc_b + tile * a.sc_s + h * a.sc_h + threadIdx.x * a.sc_d;
           if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
           else a.scale[si] = sc;
         }
       }
       __syncthreads();
     }
-    if (qm == LBFQ_Q_CHANNEL_AMAX) return;
+    if constexpr (QM == LBFQ_Q_CHANNEL_AMAX) return;
   }
 
   // ---- pass 2 (or the only pass): transform, quantise, write -------------
-  if (qm == LBFQ_Q_CHANNEL && tile == 0 && threadIdx.x < a.D && a.scale) {
-    float m = __uint_as_float(a.amax_table[(b * a.H + h) * a.D + threadIdx.x]);
-    a.scale[b * a.sc_b + h * a.sc_h + threadIdx.x * a.sc_d] = m / kFp8Max;
+  if constexpr (QM == LBFQ_Q_CHANNEL) {
+    if (tile == 0 && threadIdx.x < a.D && a.scale) {
+      const float m = __uint_as_float(a.amax_table[bh * a.D + threadIdx.x]);
+      a.scale[b * a.sc_b + h * a.sc_h + threadIdx.x * a.sc_d] = m / kFp8Max;
+    }
   }
-  for (int r0 = 0; r0 < a.R; r0 += rpp) {
-    int r = r0 + wave * rpw + row_in_wave;
-    int64_t s = s0 + r;
-    bool valid = r < a.R && s < a.S;
-    transform8(a, b, h, s, valid, d0, lpr, v, true);
-    if (qm == LBFQ_Q_NONE) continue;
-    float sc8[8];
-    if (qm == LBFQ_Q_FP8_BLOCK) {
+  // Per-column (channel) scales, or the block / MX-V scales from LDS.  Arbitrary
+  // scales divide (the reference's IEEE x / s); power-of-two scales multiply by
+  // 2^-e, which is the same correctly rounded quotient.
+  float sc8[8], rc8[8];
+  if constexpr (QM == LBFQ_Q_CHANNEL) {
+    const uint32_t* t = a.amax_table + bh * a.D + d0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sc8[i] = sc_sh[0];
-    } else if (qm == LBFQ_Q_MX_V) {
+    for (int k = 0; k < 8; ++k) {
+      sc8[k] = __uint_as_float(t[k]) / kFp8Max;
+      rc8[k] = 1.0f / sc8[k];
+    }
+  } else if constexpr (QM == LBFQ_Q_FP8_BLOCK) {
+    const float sc = sc_sh[0], rc = 1.0f / sc;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sc8[i] = sc_sh[d0 + i];
-    } else if (qm == LBFQ_Q_CHANNEL) {
-      const uint32_t* t = a.amax_table + (b * a.H + h) * a.D + d0;
+    for (int k = 0; k < 8; ++k) { sc8[k] = sc; rc8[k] = rc; }
+  } else if constexpr (QM == LBFQ_Q_MX_V) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sc8[i] = __uint_as_float(t[i]) / kFp8Max;
-    } else {  // LBFQ_Q_MX_QK: mx_block/8 lanes share a scale
-      float m = 0.0f;
+    for (int k = 0; k < 8; ++k) sc8[k] = 1.0f / sc_sh[d0 + k];  // exact: 2^-e
+  }
+  for (int p0 = 0; p0 < npass; p0 += kBatch) {
+    if (!resident) load_batch(p0, true);
+    if constexpr (QM == LBFQ_Q_NONE) continue;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
-      const int ml = a.mx_block / 8;
-      for (int o = 1; o < ml; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      m = fmaxf(m, kAmaxFloor);
-      float sc = mx_scale_from_amax(m);
+    for (int i = 0; i < kBatch; ++i) {
+      if (p0 + i >= npass) continue;
+      const int r = (p0 + i) * rpp + wave * rpw + row_in_wave;
+      const int64_t s = s0 + r;
+      float q[8];
+      if constexpr (QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_CHANNEL) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sc8[i] = sc;
-      if (valid && (lane & (ml - 1)) == 0) {
-        int64_t si = b * a.sc_b + s * a.sc_s + h * a.sc_h + (d0 / a.mx_block) * a.sc_d;
-        if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
-        else a.scale[si] = sc;
+        for (int k = 0; k < 8; ++k) q[k] = clamp448(div_by(v[i][k], sc8[k], rc8[k]));
+      } else if constexpr (QM == LBFQ_Q_MX_V) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = clamp448(v[i][k] * sc8[k]);
+      } else {  // LBFQ_Q_MX_QK: mx_block/8 lanes share a scale
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(v[i][k]));
+        const int ml = a.mx_block / 8;
+        for (int o = 1; o < ml; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        m = fmaxf(m, kAmaxFloor);
+        const float sc = mx_scale_from_amax(m);
+        const float inv = 1.0f / sc;  // exact: 2^-e
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = clamp448(v[i][k] * inv);
+        if (ok[i] && (lane & (ml - 1)) == 0) {
+          const int64_t si = b * a.sc_b + s * a.sc_s + h * a.sc_h + (d0 / a.mx_block) * a.sc_d;
+          if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
+          else a.scale[si] = sc;
+        }
+      }
+      const uint32_t lo = cvt4_e4m3(q), hi = cvt4_e4m3(q + 4);
+      if (!ok[i]) continue;
+      if (a.codes_layout == LBFQ_LAYOUT_NHD) {
+        *reinterpret_cast<uint2*>(a.codes + ((b * a.S + s) * a.H + h) * a.D + d0) = make_uint2(lo, hi);
+      } else if (a.codes_layout == LBFQ_LAYOUT_BHSD) {
+        *reinterpret_cast<uint2*>(a.codes + (bh * a.codes_spitch + s) * a.D + d0) = make_uint2(lo, hi);
+      } else {
+        uint32_t* t = reinterpret_cast<uint32_t*>(tcodes + r * tcp + d0);
+        t[0] = lo;
+        t[1] = hi;
       }
     }
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lo |= static_cast<uint32_t>(quant_e4m3(v[i], sc8[i])) << (8 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hi |= static_cast<uint32_t>(quant_e4m3(v[4 + i], sc8[4 + i])) << (8 * i);
-    if (!valid) continue;
-    if (a.codes_layout == LBFQ_LAYOUT_NHD) {
-      *reinterpret_cast<uint2*>(a.codes + ((b * a.S + s) * a.H + h) * a.D + d0) = make_uint2(lo, hi);
-    } else if (a.codes_layout == LBFQ_LAYOUT_BHSD) {
-      *reinterpret_cast<uint2*>(a.codes + ((b * a.H + h) * a.codes_spitch + s) * a.D + d0) = make_uint2(lo, hi);
-    } else {
-      *reinterpret_cast<uint2*>(tcodes + r * a.D + d0) = make_uint2(lo, hi);
-    }
   }
-  if (qm != LBFQ_Q_NONE && a.codes_layout == LBFQ_LAYOUT_BHDS) {
-    __syncthreads();
-    // Write the tile transposed: row d of the output holds R consecutive keys.
-    int64_t nvalid = a.S - s0 < a.R ? a.S - s0 : a.R;
-    for (int e = threadIdx.x; e < a.D * a.R; e += kThreads) {
-      int d = e / a.R, r = e % a.R;
-      if (r < nvalid) a.codes[((b * a.H + h) * a.D + d) * a.codes_spitch + s0 + r] = tcodes[r * a.D + d];
+  if constexpr (QM != LBFQ_Q_NONE) {
+    if (a.codes_layout == LBFQ_LAYOUT_BHDS) {
+      __syncthreads();
+      // Write the tile transposed: output row d holds R consecutive keys.  Each
+      // thread packs 4 consecutive keys of one d (4 byte reads at pitch D + 4,
+      // spread over the banks) into one dword store.
+      const int64_t nvalid = a.S - s0 < a.R ? a.S - s0 : a.R;
+      const int rq = a.R / 4;  // dwords per output row (R is a multiple of 4)
+      for (int e = threadIdx.x; e < a.D * rq; e += kThreads) {
+        const int d = e / rq, r = (e - d * rq) * 4;
+        uint8_t* dst = a.codes + (bh * a.D + d) * a.codes_spitch + s0 + r;
+        if (r + 4 <= nvalid) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) w |= static_cast<uint32_t>(tcodes[(r + k) * tcp + d]) << (8 * k);
+          *reinterpret_cast<uint32_t*>(dst) = w;
+        } else {
+          for (int k = 0; r + k < nvalid; ++k) dst[k] = tcodes[(r + k) * tcp + d];
+        }
+      }
     }
   }
 }
@@ -307,25 +397,54 @@ __global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
 // Sequential fp64 column sums of `chunk` rows (optionally gathered).
 // mode 0: write fp64 partial sums (B, nchunk, H, D);
 // mode 1: write fp32 means fp32(sum / rows_in_chunk) (B, nchunk, H, D).
-__global__ void colsum_kernel(const void* x, int dt, int64_t B, int64_t S, int64_t H, int64_t D,
-                              int chunk, const int32_t* gather, int mode, double* part, float* mean) {
+// One thread sums 8 adjacent columns of one (b, chunk, h) over the chunk's
+// rows in order; adjacent threads take adjacent 16-byte pieces of a row
+// (columns, then heads), so a wave reads contiguous memory.  Loads of 8 rows
+// are in flight before they are added, in row order.
+template <int DT>
+__global__ void __launch_bounds__(256) colsum_kernel(const void* x, int64_t B, int64_t S, int64_t H, int64_t D,
+                                                     int chunk, const int32_t* gather, int mode, double* part,
+                                                     float* mean) {
+  const int64_t ndg = D / 8;
   const int64_t nchunk = (S + chunk - 1) / chunk;
-  int64_t bid = blockIdx.x;
-  const int64_t h = bid % H; bid /= H;
-  const int64_t c = bid % nchunk;
-  const int64_t b = bid / nchunk;
-  const int d = threadIdx.x;
-  if (d >= D) return;
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= B * nchunk * H * ndg) return;
+  const int64_t dg = t % ndg; t /= ndg;
+  const int64_t h = t % H; t /= H;
+  const int64_t c = t % nchunk;
+  const int64_t b = t / nchunk;
   const int64_t s0 = c * chunk;
   const int64_t s1 = s0 + chunk < S ? s0 + chunk : S;
-  double acc = 0.0;
-  for (int64_t s = s0; s < s1; ++s) {
-    int64_t src = gather ? gather[(b * H + h) * S + s] : s;
-    acc += static_cast<double>(load_as_f32(x, ((b * S + src) * H + h) * D + d, dt));
+  const int64_t d0 = dg * 8;
+  double acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = 0.0;
+  constexpr int kRows = 8;
+  for (int64_t sb = s0; sb < s1; sb += kRows) {
+    float v[kRows][8];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      int64_t s = sb + i < s1 ? sb + i : s0;  // a safe row past the chunk end (not added)
+      if (gather) s = gather[(b * H + h) * S + s];
+      load8t<DT>(x, ((b * S + s) * H + h) * D + d0, v[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      if (sb + i < s1) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] += static_cast<double>(v[i][k]);
+      }
+    }
   }
-  int64_t o = ((b * nchunk + c) * H + h) * D + d;
-  if (mode == 0) part[o] = acc;
-  else mean[o] = static_cast<float>(acc / static_cast<double>(s1 - s0));
+  const int64_t o = ((b * nchunk + c) * H + h) * D + d0;
+  if (mode == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) part[o + k] = acc[k];
+  } else {
+    const double n = static_cast<double>(s1 - s0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mean[o + k] = static_cast<float>(acc[k] / n);
+  }
 }
 
 // Sum the chunk partials in chunk order; mean = fp32(total / S).
@@ -391,7 +510,10 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   LBFQ_CHECK_ARG(qm != LBFQ_Q_MX_V || p->S % p->R == 0, "lbfq_rowtile: S must be divisible by the MX-V block");
   LBFQ_CHECK_ARG(qm != LBFQ_Q_MX_QK || (p->mx_block >= 8 && p->mx_block <= p->D && (p->mx_block & (p->mx_block - 1)) == 0),
                  "lbfq_rowtile: MX block along D must be a power of two in [8, D]; got %d", p->mx_block);
-  LBFQ_CHECK_ARG(p->codes_layout != LBFQ_LAYOUT_BHDS || p->R * p->D <= 65536, "lbfq_rowtile: tile too large");
+  LBFQ_CHECK_ARG(p->codes_layout != LBFQ_LAYOUT_BHDS || (p->R * (p->D + 4) <= 65536 && p->R % 4 == 0),
+                 "lbfq_rowtile: transposed tile too large or R not a multiple of 4");
+  LBFQ_CHECK_ARG(p->codes_layout != LBFQ_LAYOUT_BHDS || p->codes_spitch % 4 == 0,
+                 "lbfq_rowtile: transposed codes pitch must be a multiple of 4");
   LBFQ_CHECK_ARG(p->codes_layout == LBFQ_LAYOUT_NHD || p->codes_spitch >= p->S, "lbfq_rowtile: bad codes pitch");
   RowTileArgs a;
   a.x = p->x; a.x_dtype = p->x_dtype; a.B = p->B; a.S = p->S; a.H = p->H; a.D = p->D; a.R = p->R;
@@ -406,9 +528,24 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   int64_t ntile = (p->S + p->R - 1) / p->R;
   int64_t nblocks = p->B * p->H * ntile;
   LBFQ_CHECK_ARG(nblocks < (1ll << 31), "lbfq_rowtile: grid too large");
-  size_t shmem = p->codes_layout == LBFQ_LAYOUT_BHDS ? static_cast<size_t>(p->R * p->D) : 0;
-  hipLaunchKernelGGL(rowtile_kernel, dim3(static_cast<unsigned>(nblocks)), dim3(kThreads), shmem,
-                     static_cast<hipStream_t>(stream), a);
+  size_t shmem = p->codes_layout == LBFQ_LAYOUT_BHDS ? static_cast<size_t>(p->R * (p->D + 4)) : 0;
+  const dim3 grid(static_cast<unsigned>(nblocks)), block(kThreads);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+#define LBFQ_RT(DT, QM) hipLaunchKernelGGL((rowtile_kernel<DT, QM>), grid, block, shmem, st, a)
+#define LBFQ_RT_QM(DT)                                  \
+  switch (qm) {                                         \
+    case LBFQ_Q_NONE: LBFQ_RT(DT, LBFQ_Q_NONE); break;  \
+    case LBFQ_Q_FP8_BLOCK: LBFQ_RT(DT, LBFQ_Q_FP8_BLOCK); break; \
+    case LBFQ_Q_CHANNEL: LBFQ_RT(DT, LBFQ_Q_CHANNEL); break; \
+    case LBFQ_Q_MX_QK: LBFQ_RT(DT, LBFQ_Q_MX_QK); break; \
+    case LBFQ_Q_MX_V: LBFQ_RT(DT, LBFQ_Q_MX_V); break;  \
+    default: LBFQ_RT(DT, LBFQ_Q_CHANNEL_AMAX); break;   \
+  }
+  if (p->x_dtype == kBF16) { LBFQ_RT_QM(kBF16) }
+  else if (p->x_dtype == kF16) { LBFQ_RT_QM(kF16) }
+  else { LBFQ_RT_QM(kF32) }
+#undef LBFQ_RT_QM
+#undef LBFQ_RT
   LBFQ_LAUNCH_CHECK("lbfq_rowtile");
   return 0;
 }
@@ -417,10 +554,17 @@ extern "C" int lbfq_colsum(const void* x, int dtype, int64_t B, int64_t S, int64
                            const int32_t* gather, int mode, double* partial, float* mean, lbfq_stream_t stream) {
   LBFQ_CHECK_ARG(x && (D == 64 || D == 128) && chunk > 0 && B > 0 && S > 0 && H > 0, "lbfq_colsum: bad args");
   LBFQ_CHECK_ARG(mode == 0 ? partial != nullptr : mean != nullptr, "lbfq_colsum: missing output");
-  int64_t nchunk = (S + chunk - 1) / chunk;
-  int64_t nblocks = B * nchunk * H;
-  hipLaunchKernelGGL(colsum_kernel, dim3(static_cast<unsigned>(nblocks)), dim3(static_cast<unsigned>(D)), 0,
-                     static_cast<hipStream_t>(stream), x, dtype, B, S, H, D, chunk, gather, mode, partial, mean);
+  LBFQ_CHECK_ARG(dtype >= 0 && dtype <= 2, "lbfq_colsum: bad dtype %d", dtype);
+  const int64_t nchunk = (S + chunk - 1) / chunk;
+  const int64_t nthreads = B * nchunk * H * (D / 8);
+  const dim3 grid(static_cast<unsigned>((nthreads + 255) / 256)), block(256);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(colsum_kernel<kBF16>, grid, block, 0, st, x, B, S, H, D, chunk, gather, mode, partial, mean);
+  else if (dtype == kF16)
+    hipLaunchKernelGGL(colsum_kernel<kF16>, grid, block, 0, st, x, B, S, H, D, chunk, gather, mode, partial, mean);
+  else
+    hipLaunchKernelGGL(colsum_kernel<kF32>, grid, block, 0, st, x, B, S, H, D, chunk, gather, mode, partial, mean);
   LBFQ_LAUNCH_CHECK("lbfq_colsum");
   return 0;
 }
