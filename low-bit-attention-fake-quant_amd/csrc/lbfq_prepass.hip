@@ -138,71 +138,107 @@ __device__ __forceinline__ uint32_t cvt4_e4m3(const float q[4]) {
 
 __device__ __forceinline__ float clamp448(float q) { return __builtin_amdgcn_fmed3f(q, -kFp8Max, kFp8Max); }
 
-// Row passes (rows_per_pass rows each) whose data a thread keeps in registers:
-// a batch is loaded with all its loads in flight before any of them is used,
-// and a two-pass tile (block / MX-V scales) of up to kBatch passes is read
-// from memory once.
-constexpr int kBatch = 8;
+// ---- one wave per R-row tile ------------------------------------------------
+// A wave owns one (b, h, R-row tile): lane l holds columns d0 = 8 (l % (D/8))
+// .. d0+7 of rows rl, rl + rpw, rl + 2 rpw, ... (rpw = 64 / (D/8) rows per wave
+// pass).  Tile reductions (block amax, per-column amax) are wave reductions,
+// so a tile needs no LDS round trip and no barrier; four waves of a workgroup
+// take four adjacent (head-fastest) tiles.  A tile of up to kNpMax passes
+// whose scale depends on the whole tile stays in registers (16-bit inputs as
+// packed halves: after the transforms every value is representable in the
+// input dtype), so it is read from memory once.  Loads are issued kLB passes
+// at a time, all in flight before any is used.
+constexpr int kTileWaves = 4;
+constexpr int kNpMax = 16;
+constexpr int kLB = 4;
+constexpr int kStageRows = 64;  // rows per BHDS staging chunk (per wave)
+
+template <int DT>
+struct TileStore {  // resident tile values of one lane
+  uint32_t w[kNpMax][4];
+  __device__ __forceinline__ void put(int p, const float v[8]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t lo, hi;
+      if constexpr (DT == kBF16) { lo = f32_to_bf16_bits(v[2 * k]); hi = f32_to_bf16_bits(v[2 * k + 1]); }
+      else { lo = f32_to_f16_bits(v[2 * k]); hi = f32_to_f16_bits(v[2 * k + 1]); }
+      w[p][k] = lo | (hi << 16);
+    }
+  }
+  __device__ __forceinline__ void get(int p, float v[8]) const {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t lo = static_cast<uint16_t>(w[p][k] & 0xffffu), hi = static_cast<uint16_t>(w[p][k] >> 16);
+      if constexpr (DT == kBF16) { v[2 * k] = bf16_bits_to_f32(lo); v[2 * k + 1] = bf16_bits_to_f32(hi); }
+      else { v[2 * k] = f16_bits_to_f32(lo); v[2 * k + 1] = f16_bits_to_f32(hi); }
+    }
+  }
+};
+template <>
+struct TileStore<kF32> {
+  float f[kNpMax][8];
+  __device__ __forceinline__ void put(int p, const float v[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[p][k] = v[k];
+  }
+  __device__ __forceinline__ void get(int p, float v[8]) const {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = f[p][k];
+  }
+};
 
 template <int DT, int QM>
-__global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
-  constexpr bool TWO_PASS = QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_MX_V || QM == LBFQ_Q_CHANNEL_AMAX;
+__global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a) {
+  constexpr bool TILE_RED = QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_MX_V || QM == LBFQ_Q_CHANNEL_AMAX;
+  constexpr bool RESIDENT_MODE = QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_MX_V;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int lpr = static_cast<int>(a.D / 8);       // lanes per row
-  const int rpw = 64 / lpr;                        // rows per wave per pass
-  const int rpp = rpw * (kThreads / 64);           // rows per pass
+  const int wv = threadIdx.x >> 6;
+  const int lpr = static_cast<int>(a.D / 8);  // lanes per row
+  const int rpw = 64 / lpr;                   // rows per wave pass
   const int d0 = (lane % lpr) * 8;
-  const int row_in_wave = lane / lpr;
+  const int rl = lane / lpr;
 
   const int64_t ntile = (a.S + a.R - 1) / a.R;
-  int64_t bid = blockIdx.x;
-  const int64_t h = bid % a.H; bid /= a.H;
-  const int64_t tile = bid % ntile;
-  const int64_t b = bid / ntile;
-  const int64_t s0 = tile * a.R;
-  const int npass = (a.R + rpp - 1) / rpp;
-  const int tcp = static_cast<int>(a.D) + 4;  // LDS row pitch of the BHDS staging tile (bank spread)
+  int64_t t = static_cast<int64_t>(blockIdx.x) * kTileWaves + wv;
+  if (t >= a.B * a.H * ntile) return;  // whole wave
+  const int64_t h = t % a.H; t /= a.H;
+  const int64_t tile = t % ntile;
+  const int64_t b = t / ntile;
   const int64_t bh = b * a.H + h;
+  const int64_t s0 = tile * a.R;
+  const int np = a.R / rpw;  // passes of the tile (R is a multiple of rpw)
+  const int tcp = static_cast<int>(a.D) + 4;
+  extern __shared__ uint8_t stage_all[];  // BHDS staging: per wave kStageRows rows of tcp bytes
+  uint8_t* stage = stage_all + wv * kStageRows * tcp;
 
-  __shared__ float red[kThreads / 64][128];
-  __shared__ float sc_sh[128];
-  extern __shared__ uint8_t tcodes[];  // BHDS staging: R rows of tcp bytes
-
-  const bool resident = TWO_PASS && QM != LBFQ_Q_CHANNEL_AMAX && npass <= kBatch;
-
-  float v[kBatch][8];
-  bool ok[kBatch];
-  // load + transform row passes [p0, p0 + kBatch) into v (zeros past the tile)
-  auto load_batch = [&](int p0, bool store_smoothed) {
-    int64_t src[kBatch];
+  // ---- load + transform passes [p0, p0 + kLB) -------------------------------
+  float v[kLB][8];
+  bool ok[kLB];
+  auto load_group = [&](int p0, bool store_smoothed) {
+    int64_t src[kLB];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int r = (p0 + i) * rpp + wave * rpw + row_in_wave;
-      const int64_t s = s0 + r;
-      ok[i] = p0 + i < npass && r < a.R && s < a.S;
-      src[i] = ok[i] ? s : s0;  // a safe row for lanes past the tile
+    for (int i = 0; i < kLB; ++i) {
+      const int64_t s = s0 + (p0 + i) * rpw + rl;
+      ok[i] = p0 + i < np && s < a.S;
+      src[i] = ok[i] ? s : s0;  // a safe row (not used) past the tile
       if (a.gather) src[i] = a.gather[bh * a.S + src[i]];
     }
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      if (p0 + i < npass) load8t<DT>(a.x, ((b * a.S + src[i]) * a.H + h) * a.D + d0, v[i]);
-    }
+    for (int i = 0; i < kLB; ++i) load8t<DT>(a.x, ((b * a.S + src[i]) * a.H + h) * a.D + d0, v[i]);
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      if (p0 + i >= npass) continue;
-      const int64_t s_out = s0 + (p0 + i) * rpp + wave * rpw + row_in_wave;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[i][k] = ok[i] ? v[i][k] : 0.0f;
+    for (int i = 0; i < kLB; ++i) {
+      const int64_t s_out = ok[i] ? s0 + (p0 + i) * rpw + rl : s0;
       if (a.sub_mode != LBFQ_SUB_NONE) {
         const float* m = a.sub_mode == LBFQ_SUB_COLVEC
                              ? a.sub + bh * a.D + d0
-                             : a.sub + ((b * (a.S / a.sub_block) + (ok[i] ? s_out : s0) / a.sub_block) * a.H + h) * a.D + d0;
+                             : a.sub + ((b * (a.S / a.sub_block) + s_out / a.sub_block) * a.H + h) * a.D + d0;
         const float4 m0 = reinterpret_cast<const float4*>(m)[0], m1 = reinterpret_cast<const float4*>(m)[1];
         const float mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[i][k] = ok[i] ? round_dt<DT>(v[i][k] - mm[k]) : 0.0f;
+        for (int k = 0; k < 8; ++k) v[i][k] = round_dt<DT>(v[i][k] - mm[k]);
       }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[i][k] = ok[i] ? v[i][k] : 0.0f;
       if (store_smoothed && ok[i] && a.smoothed && a.smoothed_stage == 0)
         store8(a.smoothed, DT, ((b * a.S + s_out) * a.H + h) * a.D + d0, v[i]);
       if (a.hadamard) {
@@ -239,156 +275,177 @@ __global__ void __launch_bounds__(kThreads) rowtile_kernel(RowTileArgs a) {
     }
   };
 
-  // ---- pass 1: reductions for tile-wide scales -----------------------------
-  if constexpr (TWO_PASS) {
-    float tmax = 0.0f;
-    float cmax[8];
+  // ---- quantise one pass and write its codes -------------------------------
+  float sc8[8], rc8[8];  // per-column scale and reciprocal (block: all equal)
+  auto flush_stage = [&](int r0, int nrows) {
+    // rows [r0, r0 + nrows) of the tile are staged: write them transposed, each
+    // lane packing 4 consecutive keys of one d into a dword
+    const int64_t nvalid_all = a.S - s0 < a.R ? a.S - s0 : a.R;
+    const int64_t nvalid = nvalid_all - r0 < nrows ? nvalid_all - r0 : nrows;
+    const int rq = nrows / 4;
+    for (int e = lane; e < a.D * rq; e += 64) {
+      const int d = e / rq, r = (e - d * rq) * 4;
+      uint8_t* dst = a.codes + (bh * a.D + d) * a.codes_spitch + s0 + r0 + r;
+      if (r + 4 <= nvalid) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w |= static_cast<uint32_t>(stage[(r + k) * tcp + d]) << (8 * k);
+        *reinterpret_cast<uint32_t*>(dst) = w;
+      } else {
+        for (int k = 0; r + k < nvalid; ++k) dst[k] = stage[(r + k) * tcp + d];
+      }
+    }
+  };
+  auto quant_pass = [&](int p, const float x[8], bool valid) {
+    const int r = p * rpw + rl;
+    const int64_t s = s0 + r;
+    float q[8];
+    if constexpr (QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_CHANNEL) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) q[k] = clamp448(div_by(x[k], sc8[k], rc8[k]));
+    } else if constexpr (QM == LBFQ_Q_MX_V) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) q[k] = clamp448(x[k] * rc8[k]);  // rc8 = 2^-e exactly
+    } else {  // LBFQ_Q_MX_QK: mx_block/8 lanes of the row share a power-of-two scale
+      float m = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(x[k]));
+      const int ml = a.mx_block / 8;
+      for (int o = 1; o < ml; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      m = fmaxf(m, kAmaxFloor);
+      const float sc = mx_scale_from_amax(m);
+      const float inv = 1.0f / sc;  // exact: 2^-e
+#pragma unroll
+      for (int k = 0; k < 8; ++k) q[k] = clamp448(x[k] * inv);
+      if (valid && (lane & (ml - 1)) == 0) {
+        const int64_t si = b * a.sc_b + s * a.sc_s + h * a.sc_h + (d0 / a.mx_block) * a.sc_d;
+        if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
+        else a.scale[si] = sc;
+      }
+    }
+    const uint32_t lo = cvt4_e4m3(q), hi = cvt4_e4m3(q + 4);
+    if (a.codes_layout == LBFQ_LAYOUT_BHDS) {
+      uint32_t* st = reinterpret_cast<uint32_t*>(stage + (r % kStageRows) * tcp + d0);
+      st[0] = lo;
+      st[1] = hi;
+    } else if (valid) {
+      if (a.codes_layout == LBFQ_LAYOUT_NHD)
+        *reinterpret_cast<uint2*>(a.codes + ((b * a.S + s) * a.H + h) * a.D + d0) = make_uint2(lo, hi);
+      else
+        *reinterpret_cast<uint2*>(a.codes + (bh * a.codes_spitch + s) * a.D + d0) = make_uint2(lo, hi);
+    }
+  };
+  const int spc = kStageRows / rpw;  // passes per staging chunk
+  auto after_pass = [&](int p) {     // BHDS: flush a full (or the last) staging chunk
+    if (a.codes_layout == LBFQ_LAYOUT_BHDS && ((p + 1) % spc == 0 || p + 1 == np)) {
+      const int r0 = (p / spc) * kStageRows;
+      flush_stage(r0, (p + 1) * rpw - r0);
+    }
+  };
+
+  // ---- scales that do not depend on the tile --------------------------------
+  if constexpr (QM == LBFQ_Q_CHANNEL) {
+    const uint32_t* tb = a.amax_table + bh * a.D + d0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      sc8[k] = __uint_as_float(tb[k]) / kFp8Max;
+      rc8[k] = 1.0f / sc8[k];
+    }
+    if (tile == 0 && rl == 0 && a.scale) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a.scale[b * a.sc_b + h * a.sc_h + (d0 + k) * a.sc_d] = sc8[k];
+    }
+  }
+
+  if constexpr (TILE_RED) {
+    // ---- reductions over the tile (resident: keep the values) ---------------
+    const bool resident = RESIDENT_MODE && np <= kNpMax;
+    TileStore<DT> keep;
+    float tmax = 0.0f, cmax[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) cmax[k] = 0.0f;
-    for (int p0 = 0; p0 < npass; p0 += kBatch) {
-      load_batch(p0, resident || QM == LBFQ_Q_CHANNEL_AMAX);
+    auto reduce_group = [&]() {
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
+      for (int i = 0; i < kLB; ++i) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          const float av = ok[i] ? fabsf(v[i][k]) : 0.0f;
+          const float av = fabsf(v[i][k]);  // zero for rows past the tile
           tmax = fmaxf(tmax, av);
           cmax[k] = fmaxf(cmax[k], av);
         }
       }
+    };
+    if (resident) {
+      // pass groups at compile-time offsets, so the kept values stay in registers
+#pragma unroll
+      for (int g = 0; g < kNpMax / kLB; ++g) {
+        if (g * kLB < np) {
+          load_group(g * kLB, true);
+          reduce_group();
+#pragma unroll
+          for (int i = 0; i < kLB; ++i) keep.put(g * kLB + i, v[i]);
+        }
+      }
+    } else {
+      for (int p0 = 0; p0 < np; p0 += kLB) {
+        load_group(p0, QM == LBFQ_Q_CHANNEL_AMAX);
+        reduce_group();
+      }
     }
     if constexpr (QM == LBFQ_Q_FP8_BLOCK) {
-      tmax = wave_max(tmax);
-      if (lane == 0) red[wave][0] = tmax;
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        float m = red[0][0];
-        for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w][0]);
-        m = fmaxf(m, kAmaxFloor);
-        const float sc = m / kFp8Max;
-        sc_sh[0] = sc;
-        a.scale[b * a.sc_b + tile * a.sc_s + h * a.sc_h] = sc;
-      }
-      __syncthreads();
+      const float m = fmaxf(wave_max(tmax), kAmaxFloor);
+      const float sc = m / kFp8Max, rc = 1.0f / sc;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) { sc8[k] = sc; rc8[k] = rc; }
+      if (lane == 0) a.scale[b * a.sc_b + tile * a.sc_s + h * a.sc_h] = sc;
     } else {
-      // per-column max over rows: lanes with equal (lane % lpr) share columns
+      // per-column max over the tile: lanes with equal d0 hold the same columns
 #pragma unroll
       for (int k = 0; k < 8; ++k)
         for (int m = lpr; m < 64; m <<= 1) cmax[k] = fmaxf(cmax[k], __shfl_xor(cmax[k], m, 64));
-      if (row_in_wave == 0) {
+      if constexpr (QM == LBFQ_Q_CHANNEL_AMAX) {
+        if (rl == 0) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) red[wave][d0 + k] = cmax[k];
-      }
-      __syncthreads();
-      if (threadIdx.x < a.D) {
-        float m = red[0][threadIdx.x];
-        for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w][threadIdx.x]);
-        if constexpr (QM == LBFQ_Q_CHANNEL_AMAX) {
-          atomicMax(a.amax_table + bh * a.D + threadIdx.x, __float_as_uint(m));
-        } else {
-          m = fmaxf(m, kAmaxFloor);
-          const float sc = mx_scale_from_amax(m);
-          sc_sh[threadIdx.x] = sc;
-          const int64_t si = b * a.sc_b + tile * a.sc_s + h * a.sc_h + threadIdx.x * a.sc_d;
-          if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
-          else a.scale[si] = sc;
+          for (int k = 0; k < 8; ++k) atomicMax(a.amax_table + bh * a.D + d0 + k, __float_as_uint(cmax[k]));
+        }
+        return;
+      } else {  // MX_V
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float sc = mx_scale_from_amax(fmaxf(cmax[k], kAmaxFloor));
+          sc8[k] = sc;
+          rc8[k] = 1.0f / sc;  // exact: 2^-e
+          if (rl == 0) {
+            const int64_t si = b * a.sc_b + tile * a.sc_s + h * a.sc_h + (d0 + k) * a.sc_d;
+            if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
+            else a.scale[si] = sc;
+          }
         }
       }
-      __syncthreads();
     }
-    if constexpr (QM == LBFQ_Q_CHANNEL_AMAX) return;
+    if (resident) {
+#pragma unroll
+      for (int p = 0; p < kNpMax; ++p) {
+        if (p < np) {
+          float x[8];
+          keep.get(p, x);
+          quant_pass(p, x, s0 + p * rpw + rl < a.S);
+          after_pass(p);
+        }
+      }
+      return;
+    }
   }
 
-  // ---- pass 2 (or the only pass): transform, quantise, write -------------
-  if constexpr (QM == LBFQ_Q_CHANNEL) {
-    if (tile == 0 && threadIdx.x < a.D && a.scale) {
-      const float m = __uint_as_float(a.amax_table[bh * a.D + threadIdx.x]);
-      a.scale[b * a.sc_b + h * a.sc_h + threadIdx.x * a.sc_d] = m / kFp8Max;
-    }
-  }
-  // Per-column (channel) scales, or the block / MX-V scales from LDS.  Arbitrary
-  // scales divide (the reference's IEEE x / s); power-of-two scales multiply by
-  // 2^-e, which is the same correctly rounded quotient.
-  float sc8[8], rc8[8];
-  if constexpr (QM == LBFQ_Q_CHANNEL) {
-    const uint32_t* t = a.amax_table + bh * a.D + d0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      sc8[k] = __uint_as_float(t[k]) / kFp8Max;
-      rc8[k] = 1.0f / sc8[k];
-    }
-  } else if constexpr (QM == LBFQ_Q_FP8_BLOCK) {
-    const float sc = sc_sh[0], rc = 1.0f / sc;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) { sc8[k] = sc; rc8[k] = rc; }
-  } else if constexpr (QM == LBFQ_Q_MX_V) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) sc8[k] = 1.0f / sc_sh[d0 + k];  // exact: 2^-e
-  }
-  for (int p0 = 0; p0 < npass; p0 += kBatch) {
-    if (!resident) load_batch(p0, true);
+  // ---- streaming passes (single-pass modes, or a second read of a large tile)
+  for (int p0 = 0; p0 < np; p0 += kLB) {
+    load_group(p0, true);
     if constexpr (QM == LBFQ_Q_NONE) continue;
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      if (p0 + i >= npass) continue;
-      const int r = (p0 + i) * rpp + wave * rpw + row_in_wave;
-      const int64_t s = s0 + r;
-      float q[8];
-      if constexpr (QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_CHANNEL) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = clamp448(div_by(v[i][k], sc8[k], rc8[k]));
-      } else if constexpr (QM == LBFQ_Q_MX_V) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = clamp448(v[i][k] * sc8[k]);
-      } else {  // LBFQ_Q_MX_QK: mx_block/8 lanes share a scale
-        float m = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(v[i][k]));
-        const int ml = a.mx_block / 8;
-        for (int o = 1; o < ml; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        m = fmaxf(m, kAmaxFloor);
-        const float sc = mx_scale_from_amax(m);
-        const float inv = 1.0f / sc;  // exact: 2^-e
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = clamp448(v[i][k] * inv);
-        if (ok[i] && (lane & (ml - 1)) == 0) {
-          const int64_t si = b * a.sc_b + s * a.sc_s + h * a.sc_h + (d0 / a.mx_block) * a.sc_d;
-          if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
-          else a.scale[si] = sc;
-        }
-      }
-      const uint32_t lo = cvt4_e4m3(q), hi = cvt4_e4m3(q + 4);
-      if (!ok[i]) continue;
-      if (a.codes_layout == LBFQ_LAYOUT_NHD) {
-        *reinterpret_cast<uint2*>(a.codes + ((b * a.S + s) * a.H + h) * a.D + d0) = make_uint2(lo, hi);
-      } else if (a.codes_layout == LBFQ_LAYOUT_BHSD) {
-        *reinterpret_cast<uint2*>(a.codes + (bh * a.codes_spitch + s) * a.D + d0) = make_uint2(lo, hi);
-      } else {
-        uint32_t* t = reinterpret_cast<uint32_t*>(tcodes + r * tcp + d0);
-        t[0] = lo;
-        t[1] = hi;
-      }
-    }
-  }
-  if constexpr (QM != LBFQ_Q_NONE) {
-    if (a.codes_layout == LBFQ_LAYOUT_BHDS) {
-      __syncthreads();
-      // Write the tile transposed: output row d holds R consecutive keys.  Each
-      // thread packs 4 consecutive keys of one d (4 byte reads at pitch D + 4,
-      // spread over the banks) into one dword store.
-      const int64_t nvalid = a.S - s0 < a.R ? a.S - s0 : a.R;
-      const int rq = a.R / 4;  // dwords per output row (R is a multiple of 4)
-      for (int e = threadIdx.x; e < a.D * rq; e += kThreads) {
-        const int d = e / rq, r = (e - d * rq) * 4;
-        uint8_t* dst = a.codes + (bh * a.D + d) * a.codes_spitch + s0 + r;
-        if (r + 4 <= nvalid) {
-          uint32_t w = 0;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) w |= static_cast<uint32_t>(tcodes[(r + k) * tcp + d]) << (8 * k);
-          *reinterpret_cast<uint32_t*>(dst) = w;
-        } else {
-          for (int k = 0; r + k < nvalid; ++k) dst[k] = tcodes[(r + k) * tcp + d];
-        }
+    for (int i = 0; i < kLB; ++i) {
+      if (p0 + i < np) {
+        quant_pass(p0 + i, v[i], ok[i]);
+        after_pass(p0 + i);
       }
     }
   }
@@ -510,8 +567,7 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   LBFQ_CHECK_ARG(qm != LBFQ_Q_MX_V || p->S % p->R == 0, "lbfq_rowtile: S must be divisible by the MX-V block");
   LBFQ_CHECK_ARG(qm != LBFQ_Q_MX_QK || (p->mx_block >= 8 && p->mx_block <= p->D && (p->mx_block & (p->mx_block - 1)) == 0),
                  "lbfq_rowtile: MX block along D must be a power of two in [8, D]; got %d", p->mx_block);
-  LBFQ_CHECK_ARG(p->codes_layout != LBFQ_LAYOUT_BHDS || (p->R * (p->D + 4) <= 65536 && p->R % 4 == 0),
-                 "lbfq_rowtile: transposed tile too large or R not a multiple of 4");
+
   LBFQ_CHECK_ARG(p->codes_layout != LBFQ_LAYOUT_BHDS || p->codes_spitch % 4 == 0,
                  "lbfq_rowtile: transposed codes pitch must be a multiple of 4");
   LBFQ_CHECK_ARG(p->codes_layout == LBFQ_LAYOUT_NHD || p->codes_spitch >= p->S, "lbfq_rowtile: bad codes pitch");
@@ -526,10 +582,12 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   a.smoothed_stage = p->smoothed_stage;
   a.scale_e8m0 = p->scale_e8m0;
   int64_t ntile = (p->S + p->R - 1) / p->R;
-  int64_t nblocks = p->B * p->H * ntile;
+  const int64_t ntiles = p->B * p->H * ntile;
+  const int64_t nblocks = (ntiles + kTileWaves - 1) / kTileWaves;
   LBFQ_CHECK_ARG(nblocks < (1ll << 31), "lbfq_rowtile: grid too large");
-  size_t shmem = p->codes_layout == LBFQ_LAYOUT_BHDS ? static_cast<size_t>(p->R * (p->D + 4)) : 0;
-  const dim3 grid(static_cast<unsigned>(nblocks)), block(kThreads);
+  LBFQ_CHECK_ARG(p->R % (512 / p->D) == 0, "lbfq_rowtile: R must be a multiple of %lld", (long long)(512 / p->D));
+  size_t shmem = p->codes_layout == LBFQ_LAYOUT_BHDS ? static_cast<size_t>(kTileWaves * kStageRows * (p->D + 4)) : 0;
+  const dim3 grid(static_cast<unsigned>(nblocks)), block(kTileWaves * 64);
   const hipStream_t st = static_cast<hipStream_t>(stream);
 #define LBFQ_RT(DT, QM) hipLaunchKernelGGL((rowtile_kernel<DT, QM>), grid, block, shmem, st, a)
 #define LBFQ_RT_QM(DT)                                  \
