@@ -139,6 +139,201 @@ __global__ void __launch_bounds__(256) qmk_kernel(const float* qm, const void* k
   }
 }
 
+// bf16 inputs: K_s = bf16(K - mean) is exact in bf16, so qm . K_s runs on the
+// bf16 matrix cores (v_mfma_f32_32x32x16_bf16) with qm split into three bf16
+// pieces hi + mid + lo (= qm to 24 bits): every product is exact in fp32 and
+// the sum is accumulated in fp32, as the fp32 path does, at several times its
+// rate.  A workgroup covers 256 keys (four waves of two 32-key blocks); per
+// chunk of 32 groups its threads split qm once into LDS, and every wave reads
+// its A operands there.  A = 32 qm rows, B = 32 smoothed key rows; lane
+// (i, half) supplies dimensions 16 ks + 8 half + [0, 8) of its row in both.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// two fp32 -> packed bf16 pair (one v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+constexpr int kBfKeyBlocks = 2;  // 32-key blocks per wave
+
+// Max over the 32 lanes of each half-wave of 16 values per lane, as a
+// reduce-scatter (16 exchanges instead of 80): afterwards lane i of a half
+// returns the max over the half of value index
+//   8 * bit4(i) + 4 * bit3(i) + 2 * bit2(i) + bit1(i)
+// (lanes i and i ^ 1 return the same one).  x is clobbered.
+template <int N>  // one step: N values, exchange with lane ^ N, keep N / 2 values
+__device__ __forceinline__ void half_max_step(float (&x)[16], int li) {
+  const bool up = (li & N) != 0;
+#pragma unroll
+  for (int k = 0; k < N / 2; ++k) {
+    const float keep = up ? x[k + N / 2] : x[k];
+    const float give = up ? x[k] : x[k + N / 2];
+    x[k] = fmaxf(keep, __shfl_xor(give, N, 64));
+  }
+}
+__device__ __forceinline__ float half_max16(float (&x)[16], int li) {
+  half_max_step<16>(x, li);
+  half_max_step<8>(x, li);
+  half_max_step<4>(x, li);
+  half_max_step<2>(x, li);
+  return fmaxf(x[0], __shfl_xor(x[0], 1, 64));
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) qmk_bf16_kernel(const float* qm, const uint16_t* ks, const int32_t* gather,
+                                                       const float* mean, int64_t B, int64_t S, int64_t H,
+                                                       int64_t G, float scale, float* bias, int64_t s_pitch,
+                                                       uint32_t* rowmax_bits) {
+  constexpr int NKS = D / 16;  // MFMA k-steps
+  constexpr int KPW = 32 * kBfKeyBlocks;
+  __shared__ float wmax[kWaves][32];
+  // split qm chunk: [piece][group][dim pair], rows padded by 16 bytes so the 32
+  // rows read together by a half-wave fall in different banks
+  __shared__ __attribute__((aligned(16))) uint32_t qs[3][32][D / 2 + 4];
+  const int64_t nkb = (S + KPW * kWaves - 1) / (KPW * kWaves);
+  const int64_t bh = blockIdx.x / nkb;
+  const int64_t b = bh / H, h = bh % H;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, hf = lane >> 5;
+  const int64_t nw0 = (blockIdx.x % nkb) * (KPW * kWaves) + wave * KPW;
+  float* tb = bias ? bias + bh * G * s_pitch : nullptr;  // this head's table
+
+  // B operands: smoothed rows of the wave's keys, bf16 packed, per k-step
+  u32x4 kb[kBfKeyBlocks][NKS];
+  bool nvalid[kBfKeyBlocks];
+#pragma unroll
+  for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
+    const int64_t n = nw0 + 32 * kbi + li;
+    nvalid[kbi] = n < S;
+    const int64_t src = nvalid[kbi] ? (gather ? gather[bh * S + n] : n) : 0;
+    const uint16_t* row = ks + ((b * S + src) * H + h) * D;
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) {
+      const int d0 = 16 * st + 8 * hf;
+      const uint4 r = *reinterpret_cast<const uint4*>(row + d0);
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+        x[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+      }
+      if (mean) {
+        const float4 m0 = *reinterpret_cast<const float4*>(mean + bh * D + d0);
+        const float4 m1 = *reinterpret_cast<const float4*>(mean + bh * D + d0 + 4);
+        const float mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] -= mm[i];  // rounded to bf16 by the packing
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kb[kbi][st][i] = nvalid[kbi] ? pack_bf16(x[2 * i], x[2 * i + 1]) : 0u;
+    }
+  }
+
+  // qm chunk values of this thread: group tid / 8, dimensions
+  // [(tid % 8) * D / 8, +D/8) -- loaded one chunk ahead, all loads in flight
+  constexpr int QV = D / 8;  // values per thread per chunk
+  float4 qv[QV / 4];
+  auto load_qm = [&](int64_t g0) {
+    const int64_t gr = g0 + (tid >> 3);
+    const float* src = qm + ((b * G + (gr < G ? gr : 0)) * H + h) * D + (tid & 7) * QV;
+#pragma unroll
+    for (int i = 0; i < QV / 4; ++i)
+      qv[i] = gr < G ? reinterpret_cast<const float4*>(src)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  };
+  load_qm(0);
+  for (int64_t g0 = 0; g0 < G; g0 += 32) {
+    // ---- split the chunk's qm rows into LDS ----------------------------------
+    {
+      const int gi = tid >> 3, dp0 = (tid & 7) * (QV / 2);
+#pragma unroll
+      for (int i = 0; i < QV / 4; ++i) {
+        const float x[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
+        uint32_t ph[2], pm[2], pl[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float v0 = x[2 * j], v1 = x[2 * j + 1];
+          ph[j] = pack_bf16(v0, v1);
+          const float r0 = v0 - bf16_lo(ph[j]), r1 = v1 - bf16_hi(ph[j]);  // exact
+          pm[j] = pack_bf16(r0, r1);
+          pl[j] = pack_bf16(r0 - bf16_lo(pm[j]), r1 - bf16_hi(pm[j]));  // exact residual, rounded
+        }
+        const int dp = dp0 + 2 * i;
+        *reinterpret_cast<uint2*>(&qs[0][gi][dp]) = make_uint2(ph[0], ph[1]);
+        *reinterpret_cast<uint2*>(&qs[1][gi][dp]) = make_uint2(pm[0], pm[1]);
+        *reinterpret_cast<uint2*>(&qs[2][gi][dp]) = make_uint2(pl[0], pl[1]);
+      }
+    }
+    __syncthreads();
+    if (g0 + 32 < G) load_qm(g0 + 32);  // next chunk, in flight during the MFMAs
+    v16f acc[kBfKeyBlocks];
+#pragma unroll
+    for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[kbi][r] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) {
+      const int dp = (16 * st + 8 * hf) / 2;
+      const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[2][li][dp]));
+      const bf16x8 am = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[1][li][dp]));
+      const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[0][li][dp]));
+#pragma unroll
+      for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
+        const bf16x8 bb = __builtin_bit_cast(bf16x8, kb[kbi][st]);
+        acc[kbi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bb, acc[kbi], 0, 0, 0);
+        acc[kbi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bb, acc[kbi], 0, 0, 0);
+        acc[kbi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bb, acc[kbi], 0, 0, 0);
+      }
+    }
+    // accumulator register r of lane (li, hf): group g0 + 8*(r/4) + 4*hf + r%4, key (block) + li
+    float gmax[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) gmax[r] = -INFINITY;
+    // table offsets (32-bit, within this head's table): row g0 + 4 hf + c_r,
+    // c_r = 8 (r / 4) + r % 4, column key
+    const bool full = nw0 + KPW <= S && g0 + 32 <= G;  // wave-uniform
+    const uint32_t sp = static_cast<uint32_t>(s_pitch);
+#pragma unroll
+    for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
+      const int64_t n = nw0 + 32 * kbi + li;
+      const uint32_t o0 = static_cast<uint32_t>((g0 + 4 * hf) * s_pitch + n);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float v = acc[kbi][r] * scale;
+        const uint32_t o = o0 + static_cast<uint32_t>(8 * (r >> 2) + (r & 3)) * sp;
+        float* dst = reinterpret_cast<float*>(reinterpret_cast<char*>(tb) + (o << 2));  // 32-bit byte offset
+        if (tb) {
+          if (full) {
+            *dst = v;
+          } else {
+            const int64_t g = g0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            if (nvalid[kbi] && g < G) *dst = v;
+          }
+        }
+        gmax[r] = fmaxf(gmax[r], nvalid[kbi] ? v : -INFINITY);
+      }
+    }
+    if (rowmax_bits) {
+      const float m = half_max16(gmax, li);  // max of register ridx over the half's keys
+      const int ridx = ((li >> 4) & 1) * 8 + ((li >> 3) & 1) * 4 + ((li >> 2) & 1) * 2 + ((li >> 1) & 1);
+      if ((li & 1) == 0) wmax[wave][8 * (ridx >> 2) + 4 * hf + (ridx & 3)] = m;
+    }
+    __syncthreads();  // also: every wave has read qs before it is rewritten
+    if (rowmax_bits && tid < 32 && g0 + tid < G) {
+      const float m = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
+      atomicMax(rowmax_bits + bh * G + g0 + tid, ordered_bits(m));
+    }
+  }
+}
+
 __global__ void fill_ordered_kernel(uint32_t* p, int64_t n) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = ordered_bits(-INFINITY);
@@ -164,6 +359,25 @@ extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int
   if (rb) {
     hipLaunchKernelGGL(fill_ordered_kernel, dim3(static_cast<unsigned>((nr + 255) / 256)), dim3(256), 0, st, rb, nr);
     LBFQ_LAUNCH_CHECK("lbfq_qmk fill");
+  }
+  // bf16 K: the bf16 matrix-core kernel (its table offsets within one head are 32-bit)
+  if (ks_dtype == kBF16 && (!bias || G * s_pitch * 4 < (int64_t{1} << 32))) {
+    const int64_t kpb = 32 * kBfKeyBlocks * kWaves;
+    const int64_t nb = B * H * ((S + kpb - 1) / kpb);
+    LBFQ_CHECK_ARG(nb < (int64_t{1} << 31), "lbfq_qmk: grid too large");
+    const uint16_t* k16 = static_cast<const uint16_t*>(ks);
+    if (D == 128)
+      hipLaunchKernelGGL(qmk_bf16_kernel<128>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm, k16, gather,
+                         ks_mean, B, S, H, G, scale, bias, s_pitch, rb);
+    else
+      hipLaunchKernelGGL(qmk_bf16_kernel<64>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm, k16, gather,
+                         ks_mean, B, S, H, G, scale, bias, s_pitch, rb);
+    LBFQ_LAUNCH_CHECK("lbfq_qmk");
+    if (rb) {
+      hipLaunchKernelGGL(decode_ordered_kernel, dim3(static_cast<unsigned>((nr + 255) / 256)), dim3(256), 0, st, rb, nr);
+      LBFQ_LAUNCH_CHECK("lbfq_qmk decode");
+    }
+    return 0;
   }
   const int64_t nblk = B * H * ((S + kKeysPerBlock - 1) / kKeysPerBlock);
   LBFQ_CHECK_ARG(nblk < (int64_t{1} << 31), "lbfq_qmk: grid too large");
