@@ -42,69 +42,162 @@ __global__ void km_init_kernel(const void* x, int dt, int64_t S, int64_t H, int6
   if (d < D) cent[(bh * K + j) * D + d] = load_as_f32(x, ((b * S + idx) * H + h) * D + d, dt);
 }
 
-// One thread per token; centroids of the slice in LDS.
-template <int D>
-__global__ void __launch_bounds__(256) km_assign_kernel(const void* x, int dt, int64_t S, int64_t H, int K,
-                                                        const float* cent, int32_t* labels) {
-  __shared__ float c_lds[kMaxKAssign * D];
+// n consecutive elements of dtype DT as fp32 (n a multiple of 8, 16-byte aligned)
+template <int DT, int N>
+__device__ __forceinline__ void load_row(const void* x, int64_t idx, float (&v)[N]) {
+  if constexpr (DT == kF32) {
+    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + idx);
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const float4 f = p[i];
+      v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + idx);
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+      const uint4 r = p[i];
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint16_t lo = static_cast<uint16_t>(w[k] & 0xffffu), hi = static_cast<uint16_t>(w[k] >> 16);
+        if constexpr (DT == kBF16) { v[8 * i + 2 * k] = bf16_bits_to_f32(lo); v[8 * i + 2 * k + 1] = bf16_bits_to_f32(hi); }
+        else { v[8 * i + 2 * k] = f16_bits_to_f32(lo); v[8 * i + 2 * k + 1] = f16_bits_to_f32(hi); }
+      }
+    }
+  }
+}
+
+// One thread per token: its row in registers (16-byte loads), the slice's
+// centroids in LDS read as float4 broadcasts; each distance is the sequential
+// fmaf chain over d of the specification.
+template <int D, int DT>
+__global__ void __launch_bounds__(256) km_assign_kernel(const void* x, int64_t S, int64_t H, int K, const float* cent,
+                                                        int32_t* labels) {
+  __shared__ float4 c_lds[kMaxKAssign * D / 4];
   __shared__ float cn_lds[kMaxKAssign];
   const int64_t nblk_s = (S + 255) / 256;
   const int64_t bh = blockIdx.x / nblk_s;
   const int64_t t = (blockIdx.x % nblk_s) * 256 + threadIdx.x;
   const int64_t b = bh / H, h = bh % H;
-  for (int i = threadIdx.x; i < K * D; i += 256) c_lds[i] = cent[bh * K * D + i];
+  const float4* cg = reinterpret_cast<const float4*>(cent + bh * K * D);
+  for (int i = threadIdx.x; i < K * D / 4; i += 256) c_lds[i] = cg[i];
   __syncthreads();
   if (threadIdx.x < K) {
+    const float* c = reinterpret_cast<const float*>(c_lds) + threadIdx.x * D;
     float acc = 0.0f;
-    for (int d = 0; d < D; ++d) acc = fmaf(c_lds[threadIdx.x * D + d], c_lds[threadIdx.x * D + d], acc);
+    for (int d = 0; d < D; ++d) acc = fmaf(c[d], c[d], acc);
     cn_lds[threadIdx.x] = acc;
   }
   __syncthreads();
   if (t >= S) return;
   float xv[D];
-  const int64_t base = ((b * S + t) * H + h) * D;
-#pragma unroll
-  for (int d = 0; d < D; ++d) xv[d] = load_as_f32(x, base + d, dt);
+  load_row<DT>(x, ((b * S + t) * H + h) * D, xv);
   float best = INFINITY;
   int bj = 0;
   for (int j = 0; j < K; ++j) {
-    const float* c = c_lds + j * D;
+    const float4* c = c_lds + j * (D / 4);
     float dot = 0.0f;
 #pragma unroll
-    for (int d = 0; d < D; ++d) dot = fmaf(xv[d], c[d], dot);
-    float sc = fmaf(-2.0f, dot, cn_lds[j]);
+    for (int d4 = 0; d4 < D / 4; ++d4) {
+      const float4 cv = c[d4];
+      dot = fmaf(xv[4 * d4], cv.x, dot);
+      dot = fmaf(xv[4 * d4 + 1], cv.y, dot);
+      dot = fmaf(xv[4 * d4 + 2], cv.z, dot);
+      dot = fmaf(xv[4 * d4 + 3], cv.w, dot);
+    }
+    const float sc = fmaf(-2.0f, dot, cn_lds[j]);
     if (sc < best) { best = sc; bj = j; }
   }
   labels[bh * S + t] = bj;
 }
 
-// fp64 per-cluster sums of one 1024-token chunk; one thread per column, 64
-// columns per workgroup.
-__global__ void km_update_partial_kernel(const void* x, int dt, int64_t S, int64_t H, int64_t D, int K,
-                                         const int32_t* labels, double* partial, int32_t* counts) {
-  __shared__ double sums[kMaxKAssign * 64];
-  __shared__ int cnt[kMaxKAssign];
+// fp64 per-cluster column sums of one kChunk-token chunk, D threads (one per
+// column).  The chunk's tokens are first counting-sorted by label in LDS
+// (stable, so a cluster's tokens keep their order); then each column thread
+// adds every cluster's run in that order -- the token-order fp64 sums of the
+// specification -- with the loads of 8 tokens in flight.
+template <int D, int DT>
+__global__ void __launch_bounds__(D) km_update_partial_kernel(const void* x, int64_t S, int64_t H, int K,
+                                                              const int32_t* labels, double* partial,
+                                                              int32_t* counts) {
+  constexpr int TPT = kChunk / D;  // tokens per thread in the sort
+  __shared__ int lab_s[kChunk];
+  __shared__ int ord_s[kChunk];
+  __shared__ int cnt_s[D][kMaxKAssign + 1];
+  __shared__ int start_s[kMaxKAssign + 1];
   const int64_t nchunk = (S + kChunk - 1) / kChunk;
-  const int ncg = static_cast<int>(D / 64);
-  int64_t bid = blockIdx.x;
-  const int cg = static_cast<int>(bid % ncg); bid /= ncg;
-  const int64_t bh = bid / nchunk, c = bid % nchunk;
+  const int64_t bh = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
   const int64_t b = bh / H, h = bh % H;
-  const int dl = threadIdx.x;
-  const int d = cg * 64 + dl;
-  for (int i = dl; i < K * 64; i += 64) sums[i] = 0.0;
-  for (int i = dl; i < K; i += 64) cnt[i] = 0;
+  const int th = threadIdx.x;
+  const int64_t t0 = c * kChunk;
+  const int n = static_cast<int>(t0 + kChunk < S ? kChunk : S - t0);
+  for (int i = th; i < n; i += D) lab_s[i] = labels[bh * S + t0 + i];
+  for (int j = 0; j < K; ++j) cnt_s[th][j] = 0;
   __syncthreads();
-  const int64_t t0 = c * kChunk, t1 = t0 + kChunk < S ? t0 + kChunk : S;
-  for (int64_t t = t0; t < t1; ++t) {
-    int lab = labels[bh * S + t];
-    sums[lab * 64 + dl] += static_cast<double>(load_as_f32(x, ((b * S + t) * H + h) * D + d, dt));
-    if (dl == 0) cnt[lab] += 1;
+  // per-thread counts of its TPT consecutive tokens
+#pragma unroll
+  for (int i = 0; i < TPT; ++i) {
+    const int r = th * TPT + i;
+    if (r < n) ++cnt_s[th][lab_s[r]];
   }
   __syncthreads();
-  for (int j = 0; j < K; ++j) partial[((bh * nchunk + c) * K + j) * D + d] = sums[j * 64 + dl];
-  if (cg == 0)
-    for (int i = dl; i < K; i += 64) counts[(bh * nchunk + c) * K + i] = cnt[i];
+  // per cluster: exclusive scan of the counts over threads
+  if (th < K) {
+    int run = 0;
+    for (int u = 0; u < D; ++u) {
+      const int v = cnt_s[u][th];
+      cnt_s[u][th] = run;
+      run += v;
+    }
+    start_s[th + 1] = run;  // total, made a prefix below
+  }
+  __syncthreads();
+  if (th == 0) {
+    start_s[0] = 0;
+    for (int j = 0; j < K; ++j) start_s[j + 1] += start_s[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TPT; ++i) {
+    const int r = th * TPT + i;
+    if (r < n) {
+      const int l = lab_s[r];
+      ord_s[start_s[l] + cnt_s[th][l]++] = r;
+    }
+  }
+  __syncthreads();
+  if (th < K) counts[(bh * nchunk + c) * K + th] = start_s[th + 1] - start_s[th];
+  // column sums over the sorted runs
+  double* out = partial + (bh * nchunk + c) * K * D + th;
+  const int dcol = th;
+  int j = 0;
+  double acc = 0.0;
+  constexpr int kPf = 8;
+  for (int p0 = 0; p0 < n; p0 += kPf) {
+    float v[kPf];
+#pragma unroll
+    for (int i = 0; i < kPf; ++i) {
+      const int pos = p0 + i < n ? p0 + i : n - 1;
+      v[i] = load_as_f32(x, ((b * S + t0 + ord_s[pos]) * H + h) * D + dcol, DT);
+    }
+#pragma unroll
+    for (int i = 0; i < kPf; ++i) {
+      const int pos = p0 + i;
+      if (pos < n) {
+        while (start_s[j + 1] == pos) {  // clusters ending before pos (uniform)
+          out[j * D] = acc;
+          acc = 0.0;
+          ++j;
+        }
+        acc += static_cast<double>(v[i]);
+      }
+    }
+  }
+  for (; j < K; ++j) {
+    out[j * D] = acc;
+    acc = 0.0;
+  }
 }
 
 __global__ void km_finalize_kernel(const double* partial, const int32_t* counts, int64_t nchunk, int K, int64_t D,
@@ -205,6 +298,7 @@ extern "C" int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64
                            lbfq_stream_t stream) {
   LBFQ_CHECK_ARG(x && workspace && labels && order && inverse, "lbfq_kmeans: null pointer");
   LBFQ_CHECK_ARG(D == 64 || D == 128, "lbfq_kmeans: D must be 64 or 128; got %lld", (long long)D);
+  LBFQ_CHECK_ARG(dtype >= 0 && dtype <= 2, "lbfq_kmeans: bad dtype %d", dtype);
   LBFQ_CHECK_ARG(K >= 1 && K <= S, "n_clusters must be in [1, S]; got %d for S=%lld", K, (long long)S);
   LBFQ_CHECK_ARG(K <= kMaxKAssign, "lbfq_kmeans: at most %d clusters are supported; got %d", kMaxKAssign, K);
   LBFQ_CHECK_ARG(B * H < (1ll << 31) / 1024, "lbfq_kmeans: too many slices");
@@ -218,17 +312,20 @@ extern "C" int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64
   const int64_t nblk_s = (S + 255) / 256;
   const int rounds = iters > 0 ? iters : 1;
   for (int it = 0; it < rounds; ++it) {
-    if (D == 128)
-      hipLaunchKernelGGL(km_assign_kernel<128>, dim3(static_cast<unsigned>(BH * nblk_s)), dim3(256), 0, st, x, dtype,
-                         S, H, K, w.cent, labels);
-    else
-      hipLaunchKernelGGL(km_assign_kernel<64>, dim3(static_cast<unsigned>(BH * nblk_s)), dim3(256), 0, st, x, dtype,
-                         S, H, K, w.cent, labels);
-    LBFQ_LAUNCH_CHECK("km_assign");
+    const dim3 ga(static_cast<unsigned>(BH * nblk_s)), gu(static_cast<unsigned>(BH * nchunk));
+#define LBFQ_KM(DD, DT)                                                                                     \
+  hipLaunchKernelGGL((km_assign_kernel<DD, DT>), ga, dim3(256), 0, st, x, S, H, K, w.cent, labels);          \
+  if (it + 1 < rounds)                                                                                      \
+    hipLaunchKernelGGL((km_update_partial_kernel<DD, DT>), gu, dim3(DD), 0, st, x, S, H, K, labels, w.partial, \
+                       w.counts);
+    if (D == 128) {
+      if (dtype == kBF16) { LBFQ_KM(128, kBF16) } else if (dtype == kF16) { LBFQ_KM(128, kF16) } else { LBFQ_KM(128, kF32) }
+    } else {
+      if (dtype == kBF16) { LBFQ_KM(64, kBF16) } else if (dtype == kF16) { LBFQ_KM(64, kF16) } else { LBFQ_KM(64, kF32) }
+    }
+#undef LBFQ_KM
+    LBFQ_LAUNCH_CHECK("km_assign / km_update_partial");
     if (it + 1 == rounds) break;  // the last update does not change the labels
-    hipLaunchKernelGGL(km_update_partial_kernel, dim3(static_cast<unsigned>(BH * nchunk * (D / 64))), dim3(64), 0,
-                       st, x, dtype, S, H, D, K, labels, w.partial, w.counts);
-    LBFQ_LAUNCH_CHECK("km_update_partial");
     hipLaunchKernelGGL(km_finalize_kernel, dim3(static_cast<unsigned>(BH * K)), dim3(static_cast<unsigned>(D)), 0, st,
                        w.partial, w.counts, nchunk, K, D, w.cent);
     LBFQ_LAUNCH_CHECK("km_finalize");
