@@ -112,91 +112,91 @@ __global__ void __launch_bounds__(256) km_assign_kernel(const void* x, int64_t S
   labels[bh * S + t] = bj;
 }
 
-// fp64 per-cluster column sums of one kChunk-token chunk, D threads (one per
-// column).  The chunk's tokens are first counting-sorted by label in LDS
-// (stable, so a cluster's tokens keep their order); then each column thread
-// adds every cluster's run in that order -- the token-order fp64 sums of the
-// specification -- with the loads of 8 tokens in flight.
+// fp64 per-cluster column sums of one kChunk-token chunk.  The chunk's tokens
+// are first sorted by label in LDS, stably (ballot ranks within a wave, waves
+// and rounds in token order), so a cluster's tokens keep their order.  Then
+// thread (g, d) -- column d, cluster group g -- adds the runs of clusters
+// j = g, g + NG, ... in that order: the token-order fp64 sums of the
+// specification, over chains NG times shorter, with 8 loads in flight.
+constexpr int kUpdThreads = 512;
+
 template <int D, int DT>
-__global__ void __launch_bounds__(D) km_update_partial_kernel(const void* x, int64_t S, int64_t H, int K,
-                                                              const int32_t* labels, double* partial,
-                                                              int32_t* counts) {
-  constexpr int TPT = kChunk / D;  // tokens per thread in the sort
+__global__ void __launch_bounds__(kUpdThreads) km_update_partial_kernel(const void* x, int64_t S, int64_t H, int K,
+                                                                        const int32_t* labels, double* partial,
+                                                                        int32_t* counts) {
+  constexpr int NG = kUpdThreads / D;  // cluster groups
+  constexpr int NW = kUpdThreads / 64;
   __shared__ int lab_s[kChunk];
   __shared__ int ord_s[kChunk];
-  __shared__ int cnt_s[D][kMaxKAssign + 1];
   __shared__ int start_s[kMaxKAssign + 1];
+  __shared__ int running[kMaxKAssign];
+  __shared__ int wcnt[NW][kMaxKAssign];
   const int64_t nchunk = (S + kChunk - 1) / kChunk;
   const int64_t bh = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
   const int64_t b = bh / H, h = bh % H;
-  const int th = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = c * kChunk;
   const int n = static_cast<int>(t0 + kChunk < S ? kChunk : S - t0);
-  for (int i = th; i < n; i += D) lab_s[i] = labels[bh * S + t0 + i];
-  for (int j = 0; j < K; ++j) cnt_s[th][j] = 0;
+  for (int i = tid; i < K; i += kUpdThreads) { start_s[i + 1] = 0; running[i] = 0; }
+  for (int i = tid; i < NW * K; i += kUpdThreads) wcnt[i / K][i % K] = 0;
+  for (int i = tid; i < n; i += kUpdThreads) lab_s[i] = labels[bh * S + t0 + i];
   __syncthreads();
-  // per-thread counts of its TPT consecutive tokens
-#pragma unroll
-  for (int i = 0; i < TPT; ++i) {
-    const int r = th * TPT + i;
-    if (r < n) ++cnt_s[th][lab_s[r]];
-  }
+  for (int i = tid; i < n; i += kUpdThreads) atomicAdd(&start_s[lab_s[i] + 1], 1);
   __syncthreads();
-  // per cluster: exclusive scan of the counts over threads
-  if (th < K) {
-    int run = 0;
-    for (int u = 0; u < D; ++u) {
-      const int v = cnt_s[u][th];
-      cnt_s[u][th] = run;
-      run += v;
-    }
-    start_s[th + 1] = run;  // total, made a prefix below
-  }
-  __syncthreads();
-  if (th == 0) {
+  if (tid == 0) {
     start_s[0] = 0;
     for (int j = 0; j < K; ++j) start_s[j + 1] += start_s[j];
   }
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < TPT; ++i) {
-    const int r = th * TPT + i;
-    if (r < n) {
-      const int l = lab_s[r];
-      ord_s[start_s[l] + cnt_s[th][l]++] = r;
+  int nbits = 1;
+  while ((1 << nbits) < K) ++nbits;
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int r0 = 0; r0 < n; r0 += kUpdThreads) {
+    const int r = r0 + tid;
+    const bool valid = r < n;
+    const int L = valid ? lab_s[r] : -1;
+    uint64_t match = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const uint64_t bal = __ballot(valid && ((L >> bit) & 1));
+      match &= (valid && ((L >> bit) & 1)) ? bal : ~bal;
     }
+    const int rank = __popcll(match & lt_mask);
+    if (valid && (match >> lane) == 1ull) wcnt[wave][L] = __popcll(match);  // the highest lane of its label
+    __syncthreads();
+    if (valid) {
+      int pos = start_s[L] + running[L] + rank;
+      for (int w = 0; w < wave; ++w) pos += wcnt[w][L];
+      ord_s[pos] = r;
+    }
+    __syncthreads();
+    for (int j = tid; j < K; j += kUpdThreads) {
+      int sum = 0;
+      for (int w = 0; w < NW; ++w) { sum += wcnt[w][j]; wcnt[w][j] = 0; }
+      running[j] += sum;
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (th < K) counts[(bh * nchunk + c) * K + th] = start_s[th + 1] - start_s[th];
-  // column sums over the sorted runs
-  double* out = partial + (bh * nchunk + c) * K * D + th;
-  const int dcol = th;
-  int j = 0;
-  double acc = 0.0;
-  constexpr int kPf = 8;
-  for (int p0 = 0; p0 < n; p0 += kPf) {
-    float v[kPf];
+  if (tid < K) counts[(bh * nchunk + c) * K + tid] = start_s[tid + 1] - start_s[tid];
+  // column sums over the sorted runs of this thread's clusters
+  const int g = tid / D, dcol = tid % D;
+  double* out = partial + (bh * nchunk + c) * K * D + dcol;
+  const int64_t xrow0 = (b * S + t0) * H + h;
+  for (int j = g; j < K; j += NG) {
+    const int p1 = start_s[j + 1];
+    double acc = 0.0;
+    constexpr int kPf = 8;
+    for (int p0 = start_s[j]; p0 < p1; p0 += kPf) {
+      float v[kPf];
 #pragma unroll
-    for (int i = 0; i < kPf; ++i) {
-      const int pos = p0 + i < n ? p0 + i : n - 1;
-      v[i] = load_as_f32(x, ((b * S + t0 + ord_s[pos]) * H + h) * D + dcol, DT);
-    }
-#pragma unroll
-    for (int i = 0; i < kPf; ++i) {
-      const int pos = p0 + i;
-      if (pos < n) {
-        while (start_s[j + 1] == pos) {  // clusters ending before pos (uniform)
-          out[j * D] = acc;
-          acc = 0.0;
-          ++j;
-        }
-        acc += static_cast<double>(v[i]);
+      for (int i = 0; i < kPf; ++i) {
+        const int pos = p0 + i < p1 ? p0 + i : p1 - 1;
+        v[i] = load_as_f32(x, (xrow0 + static_cast<int64_t>(ord_s[pos]) * H) * D + dcol, DT);
       }
+#pragma unroll
+      for (int i = 0; i < kPf; ++i)
+        if (p0 + i < p1) acc += static_cast<double>(v[i]);
     }
-  }
-  for (; j < K; ++j) {
     out[j * D] = acc;
-    acc = 0.0;
   }
 }
 
@@ -316,7 +316,8 @@ extern "C" int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64
 #define LBFQ_KM(DD, DT)                                                                                     \
   hipLaunchKernelGGL((km_assign_kernel<DD, DT>), ga, dim3(256), 0, st, x, S, H, K, w.cent, labels);          \
   if (it + 1 < rounds)                                                                                      \
-    hipLaunchKernelGGL((km_update_partial_kernel<DD, DT>), gu, dim3(DD), 0, st, x, S, H, K, labels, w.partial, \
+    hipLaunchKernelGGL((km_update_partial_kernel<DD, DT>), gu, dim3(kUpdThreads), 0, st, x, S, H, K, labels,  \
+                       w.partial,                                                                           \
                        w.counts);
     if (D == 128) {
       if (dtype == kBF16) { LBFQ_KM(128, kBF16) } else if (dtype == kF16) { LBFQ_KM(128, kF16) } else { LBFQ_KM(128, kF32) }
