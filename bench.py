@@ -181,6 +181,33 @@ def main() -> int:
     full_ms = _events_time(lambda: fake_quant_attention(qd, kd, vd, cfg), 2, 1)
     del cache
 
+    # ---- next to the path: the Wan call boundary and the diagnostics ---------
+    from low_bit_fake_quant import wan_hook
+    from low_bit_fake_quant.p_requant import p_requant_rows
+    from low_bit_fake_quant.rowmax_counters import count_rowmax_updates
+    extra = {}
+    if n_real != s:
+        wan_hook.set_quant_cfg(cfg)
+        qv, kv, vv = qd[:, :n_real], kd[:, :n_real], vd[:, :n_real]
+        extra["wan_hook_call_ms"] = _events_time(lambda: wan_hook.fake_or_sdpa_attention(qv, kv, vv), 2, 1)
+        extra["wan_hook_note"] = f"unpadded N={n_real} through the hook (pad + uncached fake_quant_attention)"
+        wan_hook.set_quant_cfg(None)
+    if cfg.qk_quant == "fp8_block" and ops.rowmax is not None:
+        cnt_ms = _events_time(lambda: count_rowmax_updates(ops, cfg, sm_scale=sm_scale, up_threshold=16.0,
+                                                           down_threshold=32.0, use_estimate=True), 3, 1)
+        c = count_rowmax_updates(ops, cfg, sm_scale=sm_scale, up_threshold=16.0, down_threshold=32.0,
+                                 use_estimate=True)
+        qk_flops = flops / 2
+        extra["rowmax_count"] = {"ms": cnt_ms, "TFLOPs": qk_flops / (cnt_ms * 1e-3) / 1e12,
+                                 "rule": "estimated up16 down32", "updates": c["updates"],
+                                 "rescales": c["rescales"], "rows_with_update": c["rows_with_update"],
+                                 "note": "QK-only pass; time includes the counter read-back"}
+    sc_probe = torch.randn(h, 256, 4096, device=dev)
+    pr_ms = _events_time(lambda: p_requant_rows(sc_probe, sm_scale=sm_scale), 5, 2)
+    extra["p_requant_rows"] = {"shape": list(sc_probe.shape), "ms": pr_ms,
+                               "GBps": sc_probe.numel() * 5 / (pr_ms * 1e-3) / 1e9}
+    del sc_probe
+
     # ---- prepass bandwidth: algorithmic bytes / time ------------------------
     elem = b * s * h * d
     g = s // cfg.q_smooth_block_size if cfg.smoothing == "full" else 0
@@ -229,6 +256,7 @@ def main() -> int:
         "e2e_cached_TFLOPs": flops / (e2e_ms * 1e-3) / 1e12,
         "full_call_ms": full_ms,
         "err_vs_oracle": err,
+        "next_to_path": extra,
     }
     print(json.dumps(line))
     return 0

@@ -161,6 +161,42 @@ typedef struct {
 
 int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t stream);
 
+/* ---- diagnostics -------------------------------------------------------------
+ * Replaces p_requant.py:44-73 (p_requant_rows, kernel :12-41).  scores is
+ * (B, M, N) of dtype `dtype` with element strides ss*; p (E4M3 bytes) has
+ * element strides ps*; row_sum and lse are (B, M) fp32, contiguous.  Per row:
+ * p = e4m3(2^((x - max) * sm_scale * log2e + p_max_offset)) (saturating),
+ * row_sum = sum p, lse = max * sm_scale + ln(row_sum) - p_max_offset * ln 2.
+ * sm_scale is double: sm_scale * log2e is folded in double and rounded once,
+ * as the reference folds its constexpr product. */
+int lbfq_p_requant_rows(const void* scores, int dtype, int64_t B, int64_t M, int64_t N, int64_t ssb, int64_t ssm,
+                        int64_t ssn, uint8_t* p, int64_t psb, int64_t psm, int64_t psn, float* row_sum, float* lse,
+                        double sm_scale, int p_max_offset, lbfq_stream_t stream);
+
+/* Replaces the diagnostic kernel bench/count_rowmax_updates_triton.py:27-171
+ * (_count_kernel) over the operands of lbfq_attention_fwd: FP8 codes BHSD
+ * with fp8_block scales, the qm correction table and row-max estimate in log2
+ * units.  Adds into counters[6] (int64, caller-zeroed): updates, rescales,
+ * upward updates, downward updates, rows with an update, max updates of one
+ * row (atomic max).  use_estimate = 0: FA4-style online rule (update when
+ * tile max - m > up); 1: qm_k estimate with up/down thresholds, mass floor
+ * and down_always as in the reference.  Key tiles are 64 keys. */
+typedef struct {
+  int64_t B, H, S, D, s_pitch;
+  const uint8_t* q_codes; const uint8_t* k_codes;   /* (B,H,s_pitch,D) E4M3     */
+  const float* q_scale; const float* k_scale;       /* (B,H,ceil(S/qk_block))   */
+  int qk_block;                                     /* fp8_block rows per scale */
+  const float* bias;                                /* (B,H,G,s_pitch) or NULL  */
+  const float* rowmax_est;                          /* (B,H,G) or NULL          */
+  int q_group;                                      /* rows per qm group        */
+  float sm_scale;
+  float up_threshold_log2, down_threshold_log2, mass_floor;
+  int down_always, use_estimate;
+  int64_t* counters;
+} lbfq_rowmax_count_params;
+
+int lbfq_rowmax_count(const lbfq_rowmax_count_params* p, lbfq_stream_t stream);
+
 /* ---- building-block self tests (GPU unit tests of compiler builtins) ------ */
 /* E4M3 conversion of n fp32 values (n even) by the hardware converter. */
 int lbfq_selftest_cvt_fp8(const float* x, int64_t n, uint8_t* out, lbfq_stream_t stream);

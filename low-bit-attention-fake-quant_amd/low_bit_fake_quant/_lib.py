@@ -83,6 +83,22 @@ class AttnParams(ctypes.Structure):
     ]
 
 
+class RowmaxCountParams(ctypes.Structure):
+    _fields_ = [
+        ("B", _i64), ("H", _i64), ("S", _i64), ("D", _i64), ("s_pitch", _i64),
+        ("q_codes", _vp), ("k_codes", _vp),
+        ("q_scale", _vp), ("k_scale", _vp),
+        ("qk_block", _i32),
+        ("bias", _vp),
+        ("rowmax_est", _vp),
+        ("q_group", _i32),
+        ("sm_scale", _f32),
+        ("up_threshold_log2", _f32), ("down_threshold_log2", _f32), ("mass_floor", _f32),
+        ("down_always", _i32), ("use_estimate", _i32),
+        ("counters", _vp),
+    ]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     "lbfq_last_error": (ctypes.c_char_p, []),
@@ -96,6 +112,9 @@ _SIGS = {
                            _vp]),
     "lbfq_qmk": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _vp]),
     "lbfq_attention_fwd": (_i32, [ctypes.POINTER(AttnParams), _vp]),
+    "lbfq_p_requant_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
+                                   ctypes.c_double, _i32, _vp]),
+    "lbfq_rowmax_count": (_i32, [ctypes.POINTER(RowmaxCountParams), _vp]),
     "lbfq_selftest_cvt_fp8": (_i32, [_vp, _i64, _vp, _vp]),
     "lbfq_selftest_mfma": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp]),
 }
