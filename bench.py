@@ -202,6 +202,16 @@ def main() -> int:
                                  "rule": "estimated up16 down32", "updates": c["updates"],
                                  "rescales": c["rescales"], "rows_with_update": c["rows_with_update"],
                                  "note": "QK-only pass; time includes the counter read-back"}
+    from low_bit_fake_quant import blasst_skip
+    hs = min(h, 8)
+    qs, ks, vs = (t[:, :, :hs] for t in (qd, kd, vd))
+    sim_s = _events_time(lambda: blasst_skip.simulate_workload(qs, ks, vs, skip_thresholds=[0.05],
+                                                               levels=[blasst_skip.LEVEL_FP8_SKIP]), 1, 0) / 1e3
+    sim = blasst_skip.simulate_workload(qs, ks, vs, skip_thresholds=[0.05], levels=[blasst_skip.LEVEL_FP8_SKIP])
+    extra["blasst_tile_sim"] = {"heads": hs, "S": s, "threshold": 0.05, "seconds": sim_s,
+                                "skip_rate": sim.skip_diagnostics[0.05].skip_rate,
+                                "note": "skip rung of the tile-skip simulator: per-head quant, scan, keep, attend"}
+    del qs, ks, vs, sim
     sc_probe = torch.randn(h, 256, 4096, device=dev)
     pr_ms = _events_time(lambda: p_requant_rows(sc_probe, sm_scale=sm_scale), 5, 2)
     extra["p_requant_rows"] = {"shape": list(sc_probe.shape), "ms": pr_ms,

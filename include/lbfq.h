@@ -197,6 +197,53 @@ typedef struct {
 
 int lbfq_rowmax_count(const lbfq_rowmax_count_params* p, lbfq_stream_t stream);
 
+/* ---- BLASST tile-skip simulator (blasst_skip.py:389-654) ---------------------
+ * Per-head static FP8 fake quant (fake_quant_per_head, blasst_skip.py:278-297):
+ * x (S, H, D) of dtype `dtype`; deq (S,H,D) fp32 = e4m3(x / scale) * scale or
+ * NULL; deq_mm the same rounded to bf16 (mm_bf16 = 1) or not, or NULL;
+ * scale (H) fp32 or NULL; amax_ws (H) workspace; counts[2] += saturated,
+ * underflowed-to-zero elements; sqerr[0] += sum (deq - x)^2 (fp64). */
+int lbfq_head_fp8_quant(const void* x, int dtype, int64_t S, int64_t H, int64_t D, float* deq, float* deq_mm,
+                        int mm_bf16, float* scale, uint32_t* amax_ws, int64_t* counts, double* sqerr,
+                        lbfq_stream_t stream);
+
+/* Score scan over (S, H, D) fp32 operands, 128-key blocks: final_max (H, S) =
+ * the row max; tile_margin / tile_bmax (H, S/128, S/128) = ordered-integer
+ * bits of max over a 128-row tile of (block max - running max) and of block
+ * max (blasst_skip.py:375-386, 497-506, 584-590).  S % 128 == 0, D in {64,128}. */
+int lbfq_blasst_scan(const float* q, const float* k, int64_t S, int64_t H, int64_t D, float sm_scale,
+                     float* final_max, uint32_t* tile_margin, uint32_t* tile_bmax, lbfq_stream_t stream);
+
+/* Tile keep masks for T thresholds (log_thresholds: device fp32, -inf for 0):
+ * keep (T, H, S/128, S/128) bytes; a tile keeping no block keeps the first
+ * block of largest tile_bmax; counts[2t] += skipped blocks, counts[2t+1] +=
+ * forced tiles (blasst_skip.py:597-612). */
+int lbfq_blasst_keep(const uint32_t* tile_margin, const uint32_t* tile_bmax, int64_t H, int64_t S,
+                     const float* log_thresholds, int T, uint8_t* keep, int64_t* counts, lbfq_stream_t stream);
+
+/* One rung of the simulator (blasst_skip.py:482-619).  mode 0: exact softmax
+ * against final_max; 1: online weights exp(s - rm) * exp(rm - M); 2: static P
+ * e4m3(exp(s - rm) * 256) / 256 * exp(rm - M) over kept blocks, unquantised
+ * denominator (keep == NULL keeps all).  P weights are rounded to bf16 before
+ * PV when round_p_bf16.  mode 2 only: dropped (H, S) = fraction of the row's
+ * unquantised mass in dropped blocks; p_counts[2] += underflowed-to-zero P,
+ * P count; p_sqerr[0] += sum (pq - p)^2. */
+typedef struct {
+  int64_t S, H, D;
+  const float* q; const float* k; const float* v;   /* (S, H, D) fp32 operands   */
+  float sm_scale;
+  int mode;
+  int round_p_bf16;
+  const float* final_max;                           /* (H, S) from the scan      */
+  const uint8_t* keep;                              /* (H, S/128, S/128) or NULL */
+  float* out;                                       /* (S, H, D) fp32            */
+  float* dropped;                                   /* (H, S) or NULL            */
+  int64_t* p_counts;                                /* [2] or NULL               */
+  double* p_sqerr;                                  /* [1] or NULL               */
+} lbfq_blasst_attend_params;
+
+int lbfq_blasst_attend(const lbfq_blasst_attend_params* p, lbfq_stream_t stream);
+
 /* ---- building-block self tests (GPU unit tests of compiler builtins) ------ */
 /* E4M3 conversion of n fp32 values (n even) by the hardware converter. */
 int lbfq_selftest_cvt_fp8(const float* x, int64_t n, uint8_t* out, lbfq_stream_t stream);

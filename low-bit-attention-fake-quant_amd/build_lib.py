@@ -33,6 +33,7 @@ UNITS = {
     "lbfq_kmeans.hip": ["-ffp-contract=off"],
     "lbfq_qmk.hip": ["-ffp-contract=off"],
     "lbfq_probe.hip": ["-ffp-contract=off"],
+    "lbfq_blasst_sim.hip": ["-ffp-contract=off"],
     "lbfq_attn.hip": [],
     "lbfq_attn_p0.hip": [],
     "lbfq_attn_p1.hip": [],

@@ -99,6 +99,22 @@ class RowmaxCountParams(ctypes.Structure):
     ]
 
 
+class BlasstAttendParams(ctypes.Structure):
+    _fields_ = [
+        ("S", _i64), ("H", _i64), ("D", _i64),
+        ("q", _vp), ("k", _vp), ("v", _vp),
+        ("sm_scale", _f32),
+        ("mode", _i32),
+        ("round_p_bf16", _i32),
+        ("final_max", _vp),
+        ("keep", _vp),
+        ("out", _vp),
+        ("dropped", _vp),
+        ("p_counts", _vp),
+        ("p_sqerr", _vp),
+    ]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     "lbfq_last_error": (ctypes.c_char_p, []),
@@ -115,6 +131,10 @@ _SIGS = {
     "lbfq_p_requant_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
                                    ctypes.c_double, _i32, _vp]),
     "lbfq_rowmax_count": (_i32, [ctypes.POINTER(RowmaxCountParams), _vp]),
+    "lbfq_head_fp8_quant": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "lbfq_blasst_scan": (_i32, [_vp, _vp, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp]),
+    "lbfq_blasst_keep": (_i32, [_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp]),
+    "lbfq_blasst_attend": (_i32, [ctypes.POINTER(BlasstAttendParams), _vp]),
     "lbfq_selftest_cvt_fp8": (_i32, [_vp, _i64, _vp, _vp]),
     "lbfq_selftest_mfma": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp]),
 }
