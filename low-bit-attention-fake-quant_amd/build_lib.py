@@ -51,10 +51,24 @@ def _compile(unit: str, extra: list[str]) -> str:
     return obj
 
 
+def _check_mfma(objs: list[str]) -> None:
+    sys.path.insert(0, HERE)
+    import mfma_check
+    if not mfma_check.tools_available():
+        print("mfma_check: ROCm LLVM tools not found; scale-operand check skipped", file=sys.stderr)
+        return
+    bad = {o: mfma_check.check_object(o) for o in objs}
+    bad = {o: b for o, b in bad.items() if b}
+    if bad:
+        lines = "\n".join(f"{os.path.basename(o)}: {x}" for o, b in bad.items() for x in b[:4])
+        raise RuntimeError("scaled MFMA reads a scale operand from its own destination registers:\n" + lines)
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=len(UNITS)) as ex:
         objs = list(ex.map(lambda kv: _compile(*kv), UNITS.items()))
+    _check_mfma(objs)
     tmp = OUT + ".tmp"
     cmd = ["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)

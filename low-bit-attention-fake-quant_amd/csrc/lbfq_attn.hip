@@ -46,9 +46,14 @@ __global__ void selftest_mfma_kernel(const uint8_t* A, const uint8_t* Bm, const 
   }
   v16f c;
   for (int r = 0; r < 16; ++r) c[r] = 0.0f;
-  if (as) c = mfma32<true>(av, bv, c, as[li * 2 + g], bs[li * 2 + g]);
+  const int sa = as ? as[li * 2 + g] : 127, sb = as ? bs[li * 2 + g] : 127;
+  if (as) c = mfma32<true>(av, bv, c, sa, sb);
   else c = mfma32<false>(av, bv, c, 0, 0);
   for (int r = 0; r < 16; ++r) C[(8 * (r >> 2) + 4 * g + (r & 3)) * 32 + li] = c[r];
+  // the scale registers stay live past the MFMA (after the stores that need its
+  // result), so they cannot be given to its destination
+  use(sa);
+  use(sb);
 }
 
 }  // namespace

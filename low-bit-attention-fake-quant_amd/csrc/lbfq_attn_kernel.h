@@ -605,8 +605,18 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
   bias_store(bias_fetch(0));
   qk_init(sc[0], 0);
   qk_init(sc[1], 1);
+  // E8M0 operands of v_mfma_scale must not share registers with the MFMA's
+  // destination.  When the accumulator input is the constant 0 (scores without
+  // bias) the compiler does not tie the destination to it and may hand it the
+  // register of a scale that dies at the MFMA.  The MX-QK scales are therefore
+  // kept live until the next step reads them (ke_live), so no MFMA of a step can
+  // be given their registers wherever it is scheduled.  (The PV MFMAs
+  // accumulate in place and are not affected.)
+  int ke_live[NQK];
 #pragma unroll
-  for (int i = 0; i < NQK; ++i) sc[i / NH] = qk_mfma(i, qk_read(0, i), sc[i / NH], qk_scale(0, i));
+  for (int i = 0; i < NQK; ++i) ke_live[i] = qk_scale(0, i);
+#pragma unroll
+  for (int i = 0; i < NQK; ++i) sc[i / NH] = qk_mfma(i, qk_read(0, i), sc[i / NH], ke_live[i]);
   __syncthreads();  // every wave has read K tile 0 and its bias rows before they are overwritten
 
   // One K/V tile per step.  Step it turns the scores of tile it (in sc) into P
@@ -646,6 +656,11 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     // only what it needs: metadata of tile it+1 (bias rows, Ct_next), the E8M0
     // scales of this step's MFMAs, the V block scale, the first operands
     const BiasIn bn = bias_fetch(nxt);
+    if constexpr (QK_MX) {
+      __builtin_amdgcn_sched_barrier(0);  // the previous step's MFMAs stay above
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) use(ke_live[i]);  // the previous step's scales end here
+    }
     int ve_p[NDB], ke_n[NQK];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) ve_p[db] = pv_scale(vprev, db);
@@ -856,6 +871,10 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     pop_prev = pop;
     pe_prev = pe;
     m2 = m_new;
+    if constexpr (QK_MX) {
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) ke_live[i] = ke_n[i];
+    }
 
     lds_publish<kCopies>();
     slot = nxt;
@@ -863,6 +882,11 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
   const int nfull = (S % kTN) ? nt - 1 : nt;
   for (int it = 0; it < nfull; ++it) step(it, std::false_type{});
   if (nfull < nt) step(nt - 1, std::true_type{});
+  if constexpr (QK_MX) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) use(ke_live[i]);  // the last step's scales
+  }
   // PV of the last tile; no copy is left in flight when the workgroup ends
   {
     const int vl = (nt - 1) & 3;
