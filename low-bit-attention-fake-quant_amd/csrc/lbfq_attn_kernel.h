@@ -880,7 +880,18 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     slot = nxt;
   };
   const int nfull = (S % kTN) ? nt - 1 : nt;
-  for (int it = 0; it < nfull; ++it) step(it, std::false_type{});
+  if constexpr (!QK_MX) {
+    // two steps per iteration: the loop-carried scores, P codes and ring state
+    // alternate between two register sets instead of being copied at the back edge
+    int it0 = 0;
+    for (; it0 + 1 < nfull; it0 += 2) {
+      step(it0, std::false_type{});
+      step(it0 + 1, std::false_type{});
+    }
+    if (it0 < nfull) step(it0, std::false_type{});
+  } else {
+    for (int it = 0; it < nfull; ++it) step(it, std::false_type{});
+  }
   if (nfull < nt) step(nt - 1, std::true_type{});
   if constexpr (QK_MX) {
     __builtin_amdgcn_sched_barrier(0);

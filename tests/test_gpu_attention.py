@@ -227,3 +227,20 @@ def test_blasst_is_deterministic(gpu):
                p_quant="dynamic", rowmax_mode="qm_k", blasst_lambda=0.05, blasst_fill="uta16_a1.5")
     q, k, v = (t.to(gpu) for t in _inputs(n=4096, seed=32, field=(4, 32, 32)))
     assert torch.equal(fake_quant_attention(q, k, v, cfg), fake_quant_attention(q, k, v, cfg))
+
+
+def test_blasst_rows_with_every_block_skipped_match_oracle(gpu):
+    """With the qm_k estimate above every tile max by more than |ln lambda|, a
+    row can skip all its blocks; with the zero fill its mass is 0 and the
+    reference's output row is 0/0.  The kernel's non-finite rows are exactly
+    the oracle's and the finite rows keep parity."""
+    from low_bit_fake_quant import fake_quant_attention
+    cfg = _cfg(qk_quant="fp8_block", fp8_block_size=64, smoothing="full", q_smooth_block_size=256, q_kmeans_k=16,
+               p_quant="dynamic", rowmax_mode="qm_k", blasst_lambda=0.05, blasst_fill="zero")
+    q, k, v = _inputs(n=1024, d=128, seed=24, q_clusters=4, v_bias=True, field=(4, 16, 16))
+    out = fake_quant_attention(q.to(gpu), k.to(gpu), v.to(gpu), cfg).cpu()
+    ref = opipe.fake_quant_attention(q, k, v, cfg)
+    bad_o, bad_r = ~torch.isfinite(out).all(-1), ~torch.isfinite(ref).all(-1)
+    assert bad_r.any() and torch.equal(bad_o, bad_r)
+    keep = ~bad_r
+    assert cosine(out[keep], ref[keep]) >= COS_MIN
