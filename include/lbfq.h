@@ -117,10 +117,11 @@ int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64
  * K_s = round_to_dtype(ks[gather[n]] - ks_mean) when ks_mean (B,H,D) fp32 is
  * given (ks is then the raw NHD K), else ks itself (already smoothed); gather
  * (the V-kmeans order) may be NULL.  bias is (B,H,G,s_pitch) (NULL to skip),
- * rowmax (B,H,G) (NULL to skip). */
+ * rowmax (B,H,G) (NULL to skip).  qm_split: caller workspace of B*H*3*G*(D/2)
+ * 32-bit words (qm split into bf16 hi/mid/lo), required for bf16 K. */
 int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, const float* ks_mean, int64_t B,
              int64_t S, int64_t H, int64_t D, int64_t G, float scale, float* bias, int64_t s_pitch, float* rowmax,
-             lbfq_stream_t stream);
+             uint32_t* qm_split, lbfq_stream_t stream);
 
 /* ---- FP8-MFMA P-requant attention ------------------------------------------
  * Replaces fake_quant_attention_triton (attention_triton.py:410-671) and its

@@ -186,17 +186,67 @@ __device__ __forceinline__ float half_max16(float (&x)[16], int li) {
   return fmaxf(x[0], __shfl_xor(x[0], 1, 64));
 }
 
+// qm rows split into three bf16 pieces hi + mid + lo (qm to 24 bits), once per
+// (b, h, group): out[((b*H + h)*3 + piece)*G + g][dp] holds the bf16 pair of
+// dimensions 2 dp, 2 dp + 1 (low half = even dimension).
 template <int D>
-__global__ void __launch_bounds__(256) qmk_bf16_kernel(const float* qm, const uint16_t* ks, const int32_t* gather,
-                                                       const float* mean, int64_t B, int64_t S, int64_t H,
-                                                       int64_t G, float scale, float* bias, int64_t s_pitch,
-                                                       uint32_t* rowmax_bits) {
+__global__ void __launch_bounds__(256) qm_split_kernel(const float* qm, int64_t B, int64_t H, int64_t G,
+                                                       uint32_t* out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // over B*H*G*(D/2)
+  if (i >= B * H * G * (D / 2)) return;
+  const int dp = static_cast<int>(i % (D / 2));
+  const int64_t r = i / (D / 2);
+  const int64_t g = r % G, bh = r / G;
+  const int64_t b = bh / H, h = bh % H;
+  const float2 x = *reinterpret_cast<const float2*>(qm + ((b * G + g) * H + h) * D + 2 * dp);
+  const uint32_t ph = pack_bf16(x.x, x.y);
+  const float r0 = x.x - bf16_lo(ph), r1 = x.y - bf16_hi(ph);  // exact
+  const uint32_t pm = pack_bf16(r0, r1);
+  const uint32_t pl = pack_bf16(r0 - bf16_lo(pm), r1 - bf16_hi(pm));  // exact residual, rounded
+  uint32_t* o = out + (bh * 3 * G + g) * (D / 2) + dp;
+  o[0] = ph;
+  o[G * (D / 2)] = pm;
+  o[2 * G * (D / 2)] = pl;
+}
+
+// One chunk of split qm rows (32 groups x 3 pieces, D/2 words each) moved as
+// 16-byte pieces: thread tid handles pieces tid, tid + 256, ...; rows past G
+// are clamped to G - 1 (loads stay in bounds; those rows are never stored).
+template <int D>
+__device__ __forceinline__ void qm_chunk_load(u32x4 (&qv)[3 * 32 * (D / 8) / 256], const uint32_t* qh, int g0, int G,
+                                              int tid) {
+  constexpr int C4 = D / 8;
+#pragma unroll
+  for (int i = 0; i < 3 * 32 * C4 / 256; ++i) {
+    const int e = i * 256 + tid;
+    const int piece = e / (32 * C4), row = (e / C4) % 32, c4 = e % C4;
+    const int g = min(g0 + row, G - 1);
+    qv[i] = *reinterpret_cast<const u32x4*>(qh + (piece * G + g) * (D / 2) + 4 * c4);
+  }
+}
+template <int D>
+__device__ __forceinline__ void qm_chunk_stage(const u32x4 (&qv)[3 * 32 * (D / 8) / 256], uint32_t* buf, int tid) {
+  constexpr int C4 = D / 8;
+#pragma unroll
+  for (int i = 0; i < 3 * 32 * C4 / 256; ++i) {
+    const int e = i * 256 + tid;
+    const int piece = e / (32 * C4), row = (e / C4) % 32, c4 = e % C4;
+    *reinterpret_cast<u32x4*>(buf + (piece * 32 + row) * (D / 2 + 4) + 4 * c4) = qv[i];
+  }
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) qmk_bf16_kernel(const uint32_t* qsplit, const uint16_t* ks,
+                                                       const int32_t* gather, const float* mean, int64_t B, int64_t S,
+                                                       int64_t H, int64_t G, float scale, float* bias,
+                                                       int64_t s_pitch, uint32_t* rowmax_bits) {
   constexpr int NKS = D / 16;  // MFMA k-steps
   constexpr int KPW = 32 * kBfKeyBlocks;
-  __shared__ float wmax[kWaves][32];
-  // split qm chunk: [piece][group][dim pair], rows padded by 16 bytes so the 32
-  // rows read together by a half-wave fall in different banks
-  __shared__ __attribute__((aligned(16))) uint32_t qs[3][32][D / 2 + 4];
+  __shared__ float wmax[2][kWaves][32];
+  // split qm chunks, double-buffered: [buffer][piece][group][dim pair], rows
+  // padded by 16 bytes so the 32 rows read together by a half-wave fall in
+  // different banks
+  __shared__ __attribute__((aligned(16))) uint32_t qs[2][3][32][D / 2 + 4];
   const int64_t nkb = (S + KPW * kWaves - 1) / (KPW * kWaves);
   const int64_t bh = blockIdx.x / nkb;
   const int64_t b = bh / H, h = bh % H;
@@ -238,42 +288,27 @@ __global__ void __launch_bounds__(256) qmk_bf16_kernel(const float* qm, const ui
     }
   }
 
-  // qm chunk values of this thread: group tid / 8, dimensions
-  // [(tid % 8) * D / 8, +D/8) -- loaded one chunk ahead, all loads in flight
-  constexpr int QV = D / 8;  // values per thread per chunk
-  float4 qv[QV / 4];
-  auto load_qm = [&](int64_t g0) {
-    const int64_t gr = g0 + (tid >> 3);
-    const float* src = qm + ((b * G + (gr < G ? gr : 0)) * H + h) * D + (tid & 7) * QV;
-#pragma unroll
-    for (int i = 0; i < QV / 4; ++i)
-      qv[i] = gr < G ? reinterpret_cast<const float4*>(src)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  };
-  load_qm(0);
-  for (int64_t g0 = 0; g0 < G; g0 += 32) {
-    // ---- split the chunk's qm rows into LDS ----------------------------------
-    {
-      const int gi = tid >> 3, dp0 = (tid & 7) * (QV / 2);
-#pragma unroll
-      for (int i = 0; i < QV / 4; ++i) {
-        const float x[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
-        uint32_t ph[2], pm[2], pl[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float v0 = x[2 * j], v1 = x[2 * j + 1];
-          ph[j] = pack_bf16(v0, v1);
-          const float r0 = v0 - bf16_lo(ph[j]), r1 = v1 - bf16_hi(ph[j]);  // exact
-          pm[j] = pack_bf16(r0, r1);
-          pl[j] = pack_bf16(r0 - bf16_lo(pm[j]), r1 - bf16_hi(pm[j]));  // exact residual, rounded
-        }
-        const int dp = dp0 + 2 * i;
-        *reinterpret_cast<uint2*>(&qs[0][gi][dp]) = make_uint2(ph[0], ph[1]);
-        *reinterpret_cast<uint2*>(&qs[1][gi][dp]) = make_uint2(pm[0], pm[1]);
-        *reinterpret_cast<uint2*>(&qs[2][gi][dp]) = make_uint2(pl[0], pl[1]);
-      }
-    }
-    __syncthreads();
-    if (g0 + 32 < G) load_qm(g0 + 32);  // next chunk, in flight during the MFMAs
+  // Split qm chunks (32 groups x 3 pieces) of this head, moved as 16-byte
+  // pieces: loaded into registers one chunk ahead and written into the other
+  // LDS buffer right after the chunk's MFMAs, before the chunk's table stores
+  // are issued.  Stores and loads share one completion counter, so the wait
+  // for those loads covers only stores of the previous chunk, which have had a
+  // whole chunk of MFMAs to drain.
+  constexpr int C4 = D / 8;                          // 16-byte pieces per split row
+  constexpr int NCP = 3 * 32 * C4 / 256;             // pieces per thread per chunk
+  static_assert(NCP * 256 == 3 * 32 * C4, "chunk copy must tile the workgroup");
+  const int Gi = static_cast<int>(G);
+  u32x4 qv[NCP];
+  const uint32_t* qh = qsplit + bh * 3 * G * (D / 2);
+  const int nch = (Gi + 31) / 32;
+  const bool keys_full = nw0 + KPW <= S;  // wave-uniform
+  const uint32_t sp = static_cast<uint32_t>(s_pitch);
+  qm_chunk_load<D>(qv, qh, 0, Gi, tid);
+  qm_chunk_stage<D>(qv, &qs[0][0][0][0], tid);
+  __syncthreads();
+  qm_chunk_load<D>(qv, qh, 32, Gi, tid);  // rows are clamped to G - 1, so these loads are always in bounds
+  for (int c = 0; c < nch; ++c) {
+    const int g0 = 32 * c, buf = c & 1;
     v16f acc[kBfKeyBlocks];
 #pragma unroll
     for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi)
@@ -282,9 +317,9 @@ __global__ void __launch_bounds__(256) qmk_bf16_kernel(const float* qm, const ui
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
       const int dp = (16 * st + 8 * hf) / 2;
-      const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[2][li][dp]));
-      const bf16x8 am = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[1][li][dp]));
-      const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[0][li][dp]));
+      const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[buf][2][li][dp]));
+      const bf16x8 am = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[buf][1][li][dp]));
+      const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[buf][0][li][dp]));
 #pragma unroll
       for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
         const bf16x8 bb = __builtin_bit_cast(bf16x8, kb[kbi][st]);
@@ -293,42 +328,54 @@ __global__ void __launch_bounds__(256) qmk_bf16_kernel(const float* qm, const ui
         acc[kbi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bb, acc[kbi], 0, 0, 0);
       }
     }
-    // accumulator register r of lane (li, hf): group g0 + 8*(r/4) + 4*hf + r%4, key (block) + li
+    qm_chunk_stage<D>(qv, &qs[buf ^ 1][0][0][0], tid);  // read by the next chunk (if any), after this chunk's barrier
+    // accumulator register r of lane (li, hf): group g0 + 8*(r/4) + 4*hf + r%4, key (block) + li;
+    // table offsets (32-bit, within this head's table): row g0 + 4 hf + c_r,
+    // c_r = 8 (r / 4) + r % 4, column key
     float gmax[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) gmax[r] = -INFINITY;
-    // table offsets (32-bit, within this head's table): row g0 + 4 hf + c_r,
-    // c_r = 8 (r / 4) + r % 4, column key
-    const bool full = nw0 + KPW <= S && g0 + 32 <= G;  // wave-uniform
-    const uint32_t sp = static_cast<uint32_t>(s_pitch);
+    if (keys_full && g0 + 32 <= Gi) {
 #pragma unroll
-    for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
-      const int64_t n = nw0 + 32 * kbi + li;
-      const uint32_t o0 = static_cast<uint32_t>((g0 + 4 * hf) * s_pitch + n);
+      for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
+        const uint32_t o0 = static_cast<uint32_t>(g0 + 4 * hf) * sp + static_cast<uint32_t>(nw0 + 32 * kbi + li);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float v = acc[kbi][r] * scale;
-        const uint32_t o = o0 + static_cast<uint32_t>(8 * (r >> 2) + (r & 3)) * sp;
-        float* dst = reinterpret_cast<float*>(reinterpret_cast<char*>(tb) + (o << 2));  // 32-bit byte offset
-        if (tb) {
-          if (full) {
-            *dst = v;
-          } else {
-            const int64_t g = g0 + 8 * (r >> 2) + 4 * hf + (r & 3);
-            if (nvalid[kbi] && g < G) *dst = v;
+        for (int r = 0; r < 16; ++r) {
+          const float v = acc[kbi][r] * scale;
+          if (tb) {
+            const uint32_t o = o0 + static_cast<uint32_t>(8 * (r >> 2) + (r & 3)) * sp;
+            *reinterpret_cast<float*>(reinterpret_cast<char*>(tb) + (o << 2)) = v;  // 32-bit byte offset
           }
+          gmax[r] = fmaxf(gmax[r], v);
         }
-        gmax[r] = fmaxf(gmax[r], nvalid[kbi] ? v : -INFINITY);
+      }
+    } else {
+#pragma unroll
+      for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
+        const uint32_t o0 = static_cast<uint32_t>(g0 + 4 * hf) * sp + static_cast<uint32_t>(nw0 + 32 * kbi + li);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float v = acc[kbi][r] * scale;
+          const int g = g0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+          if (tb && nvalid[kbi] && g < Gi) {
+            const uint32_t o = o0 + static_cast<uint32_t>(8 * (r >> 2) + (r & 3)) * sp;
+            *reinterpret_cast<float*>(reinterpret_cast<char*>(tb) + (o << 2)) = v;
+          }
+          gmax[r] = fmaxf(gmax[r], nvalid[kbi] ? v : -INFINITY);
+        }
       }
     }
     if (rowmax_bits) {
       const float m = half_max16(gmax, li);  // max of register ridx over the half's keys
       const int ridx = ((li >> 4) & 1) * 8 + ((li >> 3) & 1) * 4 + ((li >> 2) & 1) * 2 + ((li >> 1) & 1);
-      if ((li & 1) == 0) wmax[wave][8 * (ridx >> 2) + 4 * hf + (ridx & 3)] = m;
+      if ((li & 1) == 0) wmax[buf][wave][8 * (ridx >> 2) + 4 * hf + (ridx & 3)] = m;
     }
-    __syncthreads();  // also: every wave has read qs before it is rewritten
-    if (rowmax_bits && tid < 32 && g0 + tid < G) {
-      const float m = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
+    // the next chunk's qm and this chunk's maxima are visible; every wave has
+    // read qs[buf] (rewritten in the chunk after next)
+    __syncthreads();
+    qm_chunk_load<D>(qv, qh, g0 + 64, Gi, tid);
+    if (rowmax_bits && tid < 32 && g0 + tid < Gi) {
+      const float m = fmaxf(fmaxf(wmax[buf][0][tid], wmax[buf][1][tid]), fmaxf(wmax[buf][2][tid], wmax[buf][3][tid]));
       atomicMax(rowmax_bits + bh * G + g0 + tid, ordered_bits(m));
     }
   }
@@ -348,7 +395,7 @@ __global__ void decode_ordered_kernel(uint32_t* p, int64_t n) {
 
 extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, const float* ks_mean,
                         int64_t B, int64_t S, int64_t H, int64_t D, int64_t G, float scale, float* bias,
-                        int64_t s_pitch, float* rowmax, lbfq_stream_t stream) {
+                        int64_t s_pitch, float* rowmax, uint32_t* qm_split, lbfq_stream_t stream) {
   LBFQ_CHECK_ARG(qm && ks && (bias || rowmax), "lbfq_qmk: null pointer");
   LBFQ_CHECK_ARG(D == 64 || D == 128, "lbfq_qmk: D must be 64 or 128");
   LBFQ_CHECK_ARG(ks_dtype >= 0 && ks_dtype <= 2, "lbfq_qmk: bad dtype %d", ks_dtype);
@@ -362,16 +409,22 @@ extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int
   }
   // bf16 K: the bf16 matrix-core kernel (its table offsets within one head are 32-bit)
   if (ks_dtype == kBF16 && (!bias || G * s_pitch * 4 < (int64_t{1} << 32))) {
+    LBFQ_CHECK_ARG(qm_split, "lbfq_qmk: bf16 K needs the qm_split workspace (B*H*3*G*D/2 words)");
     const int64_t kpb = 32 * kBfKeyBlocks * kWaves;
     const int64_t nb = B * H * ((S + kpb - 1) / kpb);
     LBFQ_CHECK_ARG(nb < (int64_t{1} << 31), "lbfq_qmk: grid too large");
     const uint16_t* k16 = static_cast<const uint16_t*>(ks);
-    if (D == 128)
-      hipLaunchKernelGGL(qmk_bf16_kernel<128>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm, k16, gather,
-                         ks_mean, B, S, H, G, scale, bias, s_pitch, rb);
-    else
-      hipLaunchKernelGGL(qmk_bf16_kernel<64>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm, k16, gather,
-                         ks_mean, B, S, H, G, scale, bias, s_pitch, rb);
+    const int64_t ns = B * H * G * (D / 2);
+    const dim3 gs(static_cast<unsigned>((ns + 255) / 256));
+    if (D == 128) {
+      hipLaunchKernelGGL(qm_split_kernel<128>, gs, dim3(256), 0, st, qm, B, H, G, qm_split);
+      hipLaunchKernelGGL(qmk_bf16_kernel<128>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm_split, k16,
+                         gather, ks_mean, B, S, H, G, scale, bias, s_pitch, rb);
+    } else {
+      hipLaunchKernelGGL(qm_split_kernel<64>, gs, dim3(256), 0, st, qm, B, H, G, qm_split);
+      hipLaunchKernelGGL(qmk_bf16_kernel<64>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm_split, k16,
+                         gather, ks_mean, B, S, H, G, scale, bias, s_pitch, rb);
+    }
     LBFQ_LAUNCH_CHECK("lbfq_qmk");
     if (rb) {
       hipLaunchKernelGGL(decode_ordered_kernel, dim3(static_cast<unsigned>((nr + 255) / 256)), dim3(256), 0, st, rb, nr);

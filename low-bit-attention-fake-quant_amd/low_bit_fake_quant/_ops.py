@@ -144,8 +144,9 @@ def qmk(qm: torch.Tensor, k: RowSource, sm_scale: float, *, s_pitch: int, want_b
     rowmax = torch.empty((b, h, g), dtype=torch.float32, device=dev) if want_rowmax else None
     qm = qm.contiguous().float()
     mean = k.sub if k.sub_mode == _lib.SUB_COLVEC else None
+    split = torch.empty((b, h, 3, g, d // 2), dtype=torch.int32, device=dev) if x.dtype == torch.bfloat16 else None
     _lib.check(lib.lbfq_qmk(qm.data_ptr(), x.data_ptr(), _dt(x), _lib.ptr(k.gather), _lib.ptr(mean), b, s, h, d, g,
-                            float(sm_scale), _lib.ptr(bias), int(s_pitch), _lib.ptr(rowmax),
+                            float(sm_scale), _lib.ptr(bias), int(s_pitch), _lib.ptr(rowmax), _lib.ptr(split),
                             _lib.stream_handle(dev)), "lbfq_qmk")
     return bias, rowmax
 
