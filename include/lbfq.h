@@ -123,6 +123,17 @@ int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gathe
              int64_t S, int64_t H, int64_t D, int64_t G, float scale, float* bias, int64_t s_pitch, float* rowmax,
              uint32_t* qm_split, lbfq_stream_t stream);
 
+/* lbfq_qmk fused with the K fp8_block quantiser (quant_triton.py:27-78,
+ * applied to K_s in attention.py:533), for bf16 K: the same table and
+ * row maxima, plus K_s's codes (B,H,k_pitch,D) E4M3 (rows >= S untouched) and
+ * block scales (B,H,S/k_block) fp32, bit-identical to lbfq_rowtile's fp8_block
+ * mode on the same K_s.  One pass over K instead of two.  k_block in
+ * {16, 32, 64}, S a multiple of it. */
+int lbfq_qmk_kquant(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, const float* ks_mean,
+                    int64_t B, int64_t S, int64_t H, int64_t D, int64_t G, float scale, float* bias, int64_t s_pitch,
+                    float* rowmax, uint32_t* qm_split, uint8_t* k_codes, int64_t k_pitch, float* k_scale,
+                    int64_t k_block, lbfq_stream_t stream);
+
 /* ---- FP8-MFMA P-requant attention ------------------------------------------
  * Replaces fake_quant_attention_triton (attention_triton.py:410-671) and its
  * kernel _fake_quant_attn_fwd_kernel (attention_triton.py:48-407), taking

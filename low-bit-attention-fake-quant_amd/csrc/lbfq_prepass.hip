@@ -127,16 +127,6 @@ __device__ __forceinline__ float round_dt(float v) {
   else return v;
 }
 
-// Encode q / sc (|q / sc| <= 448 after the clamp) with the hardware RNE
-// converter; its agreement with the reference encoder over every code,
-// midpoint, neighbour of a midpoint and the subnormal range is a GPU test.
-__device__ __forceinline__ uint32_t cvt4_e4m3(const float q[4]) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-  w = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], w, true);
-  return static_cast<uint32_t>(w);
-}
-
-__device__ __forceinline__ float clamp448(float q) { return __builtin_amdgcn_fmed3f(q, -kFp8Max, kFp8Max); }
 
 // ---- one wave per R-row tile ------------------------------------------------
 // A wave owns one (b, h, R-row tile): lane l holds columns d0 = 8 (l % (D/8))

@@ -235,11 +235,65 @@ __device__ __forceinline__ void qm_chunk_stage(const u32x4 (&qv)[3 * 32 * (D / 8
   }
 }
 
+// K fp8_block quantiser fused into the qm . K_s kernel (the smoothed rows are
+// already in registers): blocks of kblk in {16, 32, 64} keys, each inside one
+// wave's 64 keys; amax over the block's smoothed values, sc = max(amax,
+// floor) / 448, codes e4m3(clamp(K_s / sc)) with the correctly rounded
+// quotient -- the arithmetic of the row-tile quantiser (lbfq_rowtile,
+// quant mode fp8_block), so the codes and scales are the same bits.  Codes go
+// to (B,H,kpitch,D) row n, scales to (B,H,S/kblk).
+template <int D>
+__device__ __forceinline__ void kquant_wave(const u32x4 (&kb)[kBfKeyBlocks][D / 16], const bool (&nvalid)[kBfKeyBlocks],
+                                            int64_t bh, int64_t nw0, int li, int hf, int64_t S, uint8_t* kcodes,
+                                            float* kscale, int64_t kpitch, int kblk) {
+  constexpr int NKS = D / 16;
+  float am[kBfKeyBlocks];
+#pragma unroll
+  for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
+    float m = 0.0f;  // rows past S hold zeros
+#pragma unroll
+    for (int st = 0; st < NKS; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        m = fmaxf(m, fmaxf(fabsf(bf16_lo(kb[kbi][st][i])), fabsf(bf16_hi(kb[kbi][st][i]))));
+    // lanes (li, hf) and (li, hf ^ 1) hold the two halves of key li's row
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    // keys of one block: xor over the low log2(kblk) bits of li (kblk <= 32)
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1)
+      if (o < kblk) m = fmaxf(m, __shfl_xor(m, o, 64));
+    am[kbi] = m;
+  }
+  if (kblk == 64) am[0] = am[1] = fmaxf(am[0], am[1]);
+#pragma unroll
+  for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
+    const float sc = fmaxf(am[kbi], kAmaxFloor) / kFp8Max, rc = 1.0f / sc;
+    const int64_t n = nw0 + 32 * kbi + li;
+    if (nvalid[kbi]) {
+      uint8_t* row = kcodes + (bh * kpitch + n) * D;
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        float q[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          q[2 * i] = clamp448(div_by(bf16_lo(kb[kbi][st][i]), sc, rc));
+          q[2 * i + 1] = clamp448(div_by(bf16_hi(kb[kbi][st][i]), sc, rc));
+        }
+        *reinterpret_cast<uint2*>(row + 16 * st + 8 * hf) = make_uint2(cvt4_e4m3(q), cvt4_e4m3(q + 4));
+      }
+    }
+    // one lane per block writes its scale: the block's first key
+    if (hf == 0 && (li & (kblk - 1)) == 0 && n < S && (kblk < 64 || kbi == 0))
+      kscale[bh * (S / kblk) + n / kblk] = sc;
+  }
+}
+
 template <int D>
 __global__ void __launch_bounds__(256) qmk_bf16_kernel(const uint32_t* qsplit, const uint16_t* ks,
                                                        const int32_t* gather, const float* mean, int64_t B, int64_t S,
                                                        int64_t H, int64_t G, float scale, float* bias,
-                                                       int64_t s_pitch, uint32_t* rowmax_bits) {
+                                                       int64_t s_pitch, uint32_t* rowmax_bits, uint8_t* kcodes,
+                                                       float* kscale, int64_t kpitch, int kblk) {
   constexpr int NKS = D / 16;  // MFMA k-steps
   constexpr int KPW = 32 * kBfKeyBlocks;
   __shared__ float wmax[2][kWaves][32];
@@ -287,6 +341,7 @@ __global__ void __launch_bounds__(256) qmk_bf16_kernel(const uint32_t* qsplit, c
       for (int i = 0; i < 4; ++i) kb[kbi][st][i] = nvalid[kbi] ? pack_bf16(x[2 * i], x[2 * i + 1]) : 0u;
     }
   }
+  if (kcodes) kquant_wave<D>(kb, nvalid, bh, nw0, li, hf, S, kcodes, kscale, kpitch, kblk);
 
   // Split qm chunks (32 groups x 3 pieces) of this head, moved as 16-byte
   // pieces: loaded into registers one chunk ahead and written into the other
@@ -393,9 +448,12 @@ __global__ void decode_ordered_kernel(uint32_t* p, int64_t n) {
 
 }  // namespace
 
-extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, const float* ks_mean,
-                        int64_t B, int64_t S, int64_t H, int64_t D, int64_t G, float scale, float* bias,
-                        int64_t s_pitch, float* rowmax, uint32_t* qm_split, lbfq_stream_t stream) {
+namespace {
+
+int qmk_launch(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, const float* ks_mean, int64_t B,
+               int64_t S, int64_t H, int64_t D, int64_t G, float scale, float* bias, int64_t s_pitch, float* rowmax,
+               uint32_t* qm_split, uint8_t* k_codes, int64_t k_pitch, float* k_scale, int64_t k_block,
+               lbfq_stream_t stream) {
   LBFQ_CHECK_ARG(qm && ks && (bias || rowmax), "lbfq_qmk: null pointer");
   LBFQ_CHECK_ARG(D == 64 || D == 128, "lbfq_qmk: D must be 64 or 128");
   LBFQ_CHECK_ARG(ks_dtype >= 0 && ks_dtype <= 2, "lbfq_qmk: bad dtype %d", ks_dtype);
@@ -419,11 +477,13 @@ extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int
     if (D == 128) {
       hipLaunchKernelGGL(qm_split_kernel<128>, gs, dim3(256), 0, st, qm, B, H, G, qm_split);
       hipLaunchKernelGGL(qmk_bf16_kernel<128>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm_split, k16,
-                         gather, ks_mean, B, S, H, G, scale, bias, s_pitch, rb);
+                         gather, ks_mean, B, S, H, G, scale, bias, s_pitch, rb, k_codes, k_scale, k_pitch,
+                         static_cast<int>(k_block));
     } else {
       hipLaunchKernelGGL(qm_split_kernel<64>, gs, dim3(256), 0, st, qm, B, H, G, qm_split);
       hipLaunchKernelGGL(qmk_bf16_kernel<64>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm_split, k16,
-                         gather, ks_mean, B, S, H, G, scale, bias, s_pitch, rb);
+                         gather, ks_mean, B, S, H, G, scale, bias, s_pitch, rb, k_codes, k_scale, k_pitch,
+                         static_cast<int>(k_block));
     }
     LBFQ_LAUNCH_CHECK("lbfq_qmk");
     if (rb) {
@@ -432,6 +492,7 @@ extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int
     }
     return 0;
   }
+  LBFQ_CHECK_ARG(!k_codes, "lbfq_qmk_kquant: the fused K quantiser needs bf16 K and a table under 4 GiB per head");
   const int64_t nblk = B * H * ((S + kKeysPerBlock - 1) / kKeysPerBlock);
   LBFQ_CHECK_ARG(nblk < (int64_t{1} << 31), "lbfq_qmk: grid too large");
   if (D == 128)
@@ -446,4 +507,27 @@ extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int
     LBFQ_LAUNCH_CHECK("lbfq_qmk decode");
   }
   return 0;
+}
+
+}  // namespace
+
+extern "C" int lbfq_qmk(const float* qm, const void* ks, int ks_dtype, const int32_t* gather, const float* ks_mean,
+                        int64_t B, int64_t S, int64_t H, int64_t D, int64_t G, float scale, float* bias,
+                        int64_t s_pitch, float* rowmax, uint32_t* qm_split, lbfq_stream_t stream) {
+  return qmk_launch(qm, ks, ks_dtype, gather, ks_mean, B, S, H, D, G, scale, bias, s_pitch, rowmax, qm_split,
+                    nullptr, 0, nullptr, 0, stream);
+}
+
+extern "C" int lbfq_qmk_kquant(const float* qm, const void* ks, int ks_dtype, const int32_t* gather,
+                               const float* ks_mean, int64_t B, int64_t S, int64_t H, int64_t D, int64_t G,
+                               float scale, float* bias, int64_t s_pitch, float* rowmax, uint32_t* qm_split,
+                               uint8_t* k_codes, int64_t k_pitch, float* k_scale, int64_t k_block,
+                               lbfq_stream_t stream) {
+  LBFQ_CHECK_ARG(k_codes && k_scale, "lbfq_qmk_kquant: null K code / scale pointer");
+  LBFQ_CHECK_ARG(k_block == 16 || k_block == 32 || k_block == 64, "lbfq_qmk_kquant: K block must be 16, 32 or 64");
+  LBFQ_CHECK_ARG(S > 0 && S % k_block == 0 && k_pitch >= S, "lbfq_qmk_kquant: S must be a multiple of the K block");
+  LBFQ_CHECK_ARG(ks_dtype == kBF16 && (!bias || G * s_pitch * 4 < (int64_t{1} << 32)),
+                 "lbfq_qmk_kquant: the fused K quantiser needs bf16 K and a table under 4 GiB per head");
+  return qmk_launch(qm, ks, ks_dtype, gather, ks_mean, B, S, H, D, G, scale, bias, s_pitch, rowmax, qm_split,
+                    k_codes, k_pitch, k_scale, k_block, stream);
 }

@@ -127,6 +127,8 @@ _SIGS = {
     "lbfq_kmeans": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, ctypes.c_uint64, _vp, _vp, _vp, _vp,
                            _vp]),
     "lbfq_qmk": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
+    "lbfq_qmk_kquant": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _vp,
+                               _vp, _i64, _vp, _i64, _vp]),
     "lbfq_attention_fwd": (_i32, [ctypes.POINTER(AttnParams), _vp]),
     "lbfq_p_requant_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
                                    ctypes.c_double, _i32, _vp]),

@@ -126,10 +126,14 @@ def kmeans(x: torch.Tensor, k: int, iters: int, seed: int):
 
 
 def qmk(qm: torch.Tensor, k: RowSource, sm_scale: float, *, s_pitch: int, want_bias: bool = True,
-        want_rowmax: bool = True):
+        want_rowmax: bool = True, k_quant: tuple | None = None):
     """bias (B,H,G,s_pitch) = qm.K_s * sm_scale and rowmax (B,H,G) = max_n bias,
     with K_s the smoothed (and gathered) K described by ``k``: no K_s tensor is
-    materialised when ``k`` subtracts a per-(b,h) column mean."""
+    materialised when ``k`` subtracts a per-(b,h) column mean.
+
+    k_quant = (codes (B,H,P,D) uint8, scale (B,H,S/block) fp32, block): also
+    quantise K_s in fp8_block mode in the same pass (bf16 K only; the codes and
+    scales equal the row-tile quantiser's bit for bit)."""
     lib = _lib.load()
     x = k.x
     b, s, h, d = x.shape
@@ -145,9 +149,20 @@ def qmk(qm: torch.Tensor, k: RowSource, sm_scale: float, *, s_pitch: int, want_b
     qm = qm.contiguous().float()
     mean = k.sub if k.sub_mode == _lib.SUB_COLVEC else None
     split = torch.empty((b, h, 3, g, d // 2), dtype=torch.int32, device=dev) if x.dtype == torch.bfloat16 else None
-    _lib.check(lib.lbfq_qmk(qm.data_ptr(), x.data_ptr(), _dt(x), _lib.ptr(k.gather), _lib.ptr(mean), b, s, h, d, g,
-                            float(sm_scale), _lib.ptr(bias), int(s_pitch), _lib.ptr(rowmax), _lib.ptr(split),
-                            _lib.stream_handle(dev)), "lbfq_qmk")
+    if k_quant is None:
+        _lib.check(lib.lbfq_qmk(qm.data_ptr(), x.data_ptr(), _dt(x), _lib.ptr(k.gather), _lib.ptr(mean), b, s, h, d,
+                                g, float(sm_scale), _lib.ptr(bias), int(s_pitch), _lib.ptr(rowmax), _lib.ptr(split),
+                                _lib.stream_handle(dev)), "lbfq_qmk")
+    else:
+        codes, kscale, blk = k_quant
+        if codes.dtype != torch.uint8 or codes.shape[:2] != (b, h) or codes.shape[3] != d or not codes.is_contiguous():
+            raise ValueError("qmk: K codes must be a contiguous (B,H,P,D) uint8 tensor")
+        if kscale.dtype != torch.float32 or kscale.shape != (b, h, s // blk) or not kscale.is_contiguous():
+            raise ValueError("qmk: K scales must be a contiguous (B,H,S/block) fp32 tensor")
+        _lib.check(lib.lbfq_qmk_kquant(qm.data_ptr(), x.data_ptr(), _dt(x), _lib.ptr(k.gather), _lib.ptr(mean), b, s,
+                                       h, d, g, float(sm_scale), _lib.ptr(bias), int(s_pitch), _lib.ptr(rowmax),
+                                       _lib.ptr(split), codes.data_ptr(), codes.shape[2], kscale.data_ptr(), int(blk),
+                                       _lib.stream_handle(dev)), "lbfq_qmk_kquant")
     return bias, rowmax
 
 

@@ -285,19 +285,27 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
     signs = None
     if cfg.qk_hadamard and cfg.qk_hadamard_random_sign:
         signs = qk_signs_device(h, d, cfg.qk_hadamard_seed, prep.q.x.device)
-    q_codes, q_scale = _quant_qk_codes(prep.q, cfg, P, signs=signs)
-    k_codes, k_scale = _quant_qk_codes(prep.k, cfg, P, signs=signs)
-    v_codes, v_scale, v_kind, v_block = _quant_v_codes(prep.v, cfg, P)
-    bias = rowmax = None
     if cfg.rowmax_mode == "qm_k":
         if not has_qm:
             raise ValueError("rowmax_mode='qm_k' requires smoothing='full' so qm exists")
     elif cfg.rowmax_mode != "online":
         raise ValueError(f"unsupported rowmax_mode: {cfg.rowmax_mode!r}")
+    q_codes, q_scale = _quant_qk_codes(prep.q, cfg, P, signs=signs)
+    # with the qm correction, K_s is quantised inside the qm.K_s pass when it can be
+    fuse_k = has_qm and _k_quant_fusable(prep.k, cfg, P, prep.qm.shape[1])
+    if fuse_k:
+        blk = cfg.fp8_block_size
+        k_codes = (torch.zeros if P > s else torch.empty)((b, h, P, d), dtype=torch.uint8, device=prep.k.x.device)
+        k_scale = torch.empty((b, h, s // blk), dtype=torch.float32, device=prep.k.x.device)
+    else:
+        k_codes, k_scale = _quant_qk_codes(prep.k, cfg, P, signs=signs)
+    v_codes, v_scale, v_kind, v_block = _quant_v_codes(prep.v, cfg, P)
+    bias = rowmax = None
     if has_qm:
         # scores are handled in log2 units by the kernel
         # K_s = K - mean is formed inside the qm.K_s kernel (never stored)
-        bias, rowmax = qmk(prep.qm, prep.k, sm_scale * LOG2E, s_pitch=P, want_rowmax=cfg.rowmax_mode == "qm_k")
+        bias, rowmax = qmk(prep.qm, prep.k, sm_scale * LOG2E, s_pitch=P, want_rowmax=cfg.rowmax_mode == "qm_k",
+                           k_quant=(k_codes, k_scale, cfg.fp8_block_size) if fuse_k else None)
     v_alpha = None
     if prep.v_alpha is not None:
         v_alpha = prep.v_alpha.permute(0, 2, 1, 3).contiguous()
@@ -315,6 +323,15 @@ def _p_requant_hip(prep: _Prep, cfg: QuantConfig, sm_scale: float, out_dtype: to
 # ---------------------------------------------------------------------------
 # Path A: dequant Q/K/V -> attention with fp32 P (reference attention.py:247-321)
 # ---------------------------------------------------------------------------
+
+
+def _k_quant_fusable(k: RowSource, cfg: QuantConfig, P: int, groups: int) -> bool:
+    """Whether lbfq_qmk_kquant can quantise K_s in the qm.K_s pass: bf16 K,
+    fp8_block of 16/32/64 keys, no Hadamard, a table under 4 GiB per head."""
+    s = k.shape[1]
+    return (cfg.qk_quant == "fp8_block" and not cfg.qk_hadamard and k.x.dtype == torch.bfloat16
+            and cfg.fp8_block_size in (16, 32, 64) and s % cfg.fp8_block_size == 0
+            and k.sub_mode in (_lib.SUB_NONE, _lib.SUB_COLVEC) and groups * P * 4 < (1 << 32))
 
 
 def _qk_inputs_for_quant(q_work, k_work, cfg):

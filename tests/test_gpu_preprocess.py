@@ -108,3 +108,43 @@ def test_qmk_table_and_rowmax(gpu, d, gathered):
     assert ((got - ref).abs() <= 1e-6 * mag + 1e-30).all()
     assert torch.count_nonzero(bias[..., s:]) == 0
     assert torch.equal(rowmax, bias[..., :s].amax(-1))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("blk", [16, 32, 64])
+@pytest.mark.parametrize("gathered", [False, True])
+def test_qmk_fused_k_quant_matches_separate_passes(gpu, d, blk, gathered):
+    """lbfq_qmk_kquant: the qm.K_s table, row maxima, K_s codes and block scales
+    equal (bitwise) those of lbfq_qmk plus the row-tile fp8_block quantiser, and
+    the codes / scales equal the CPU oracle's fp8_block quant of K_s.  S = 960
+    leaves a partial last workgroup (256 keys each)."""
+    from oracle import quant as oq
+    from low_bit_fake_quant import _lib
+    from low_bit_fake_quant._ops import RowSource, qmk, rowtile
+    s, h, g, pitch = 960, 3, 4, 1024
+    k = (cpu_randn(1, s, h, d, seed=31) * 3 + 1.5).to(torch.bfloat16)
+    qm = cpu_randn(1, g, h, d, seed=32, dtype=torch.float32)
+    mean = opre.k_mean(k)
+    gen = torch.Generator().manual_seed(33)
+    order = torch.stack([torch.randperm(s, generator=gen) for _ in range(h)]).to(torch.int32) if gathered else None
+    src = RowSource(k.to(gpu), gather=order.to(gpu) if gathered else None, sub_mode=_lib.SUB_COLVEC,
+                    sub=mean.to(gpu))
+    nb = s // blk
+    codes_a = torch.zeros((1, h, pitch, d), dtype=torch.uint8, device=gpu)
+    scale_a = torch.empty((1, h, nb), dtype=torch.float32, device=gpu)
+    rowtile(src, R=blk, quant_mode=_lib.Q_FP8_BLOCK, codes=codes_a, codes_layout=_lib.LAYOUT_BHSD,
+            codes_spitch=pitch, scale=scale_a, scale_strides=(h * nb, 1, nb, 0))
+    bias_a, rowmax_a = qmk(qm.to(gpu), src, 0.127, s_pitch=pitch)
+    codes_b = torch.zeros((1, h, pitch, d), dtype=torch.uint8, device=gpu)
+    scale_b = torch.full((1, h, nb), -1.0, dtype=torch.float32, device=gpu)
+    bias_b, rowmax_b = qmk(qm.to(gpu), src, 0.127, s_pitch=pitch, k_quant=(codes_b, scale_b, blk))
+    assert torch.equal(codes_b, codes_a) and torch.equal(scale_b, scale_a)
+    assert torch.equal(bias_b, bias_a) and torch.equal(rowmax_b, rowmax_a)
+    # the oracle's fp8_block quant of K_s (NHD, gathered rows in output order)
+    kk = k.permute(0, 2, 1, 3)
+    if gathered:
+        kk = torch.stack([kk[0, i, order[i].long()] for i in range(h)]).unsqueeze(0)
+    ks = (kk.float() - mean[:, :, None, :]).to(torch.bfloat16).permute(0, 2, 1, 3)   # (B,S,H,D)
+    oc, osc = oq.fp8_block_quant(ks, block_s=blk)
+    assert torch.equal(codes_b.cpu()[:, :, :s], oc.permute(0, 2, 1, 3))
+    assert torch.equal(scale_b.cpu(), osc.permute(0, 2, 1))
