@@ -41,8 +41,11 @@
 // chunks of 8 keys per lane; each chunk carries one or two MFMAs that do not
 // depend on it -- the PV of tile t-1 (P codes kept in registers) and the QK of
 // tile t+1 (written into score registers the earlier chunks have consumed).
-// On gfx950 a 32x32x64 MFMA blocks most VALU issue of its SIMD while it runs,
-// so a tile costs roughly its VALU cycles plus about half of its MFMA cycles;
+// On gfx950 independent VALU work of either wave of a SIMD issues while a
+// 32x32x64 MFMA runs (each MFMA takes ~15-20 cycles of VALU issue), and the
+// softmax of a tile needs more VALU cycles than its MFMAs need matrix cycles
+// (exp, the FP8 conversion and permlane take 8 cycles per wave instruction,
+// fma / max 4, add / mul / mov 2-4), so a tile costs about its VALU cycles;
 // the interleave keeps the wave from idling on its own LDS reads and MFMA
 // results.  Empty asm fences (pin / use) and sched_barrier keep each chunk's
 // work together, and all LDS reads of a step are issued before the first
