@@ -335,7 +335,7 @@ __device__ __forceinline__ float blasst_fill(const KArgs& a, const float (&u)[32
 }
 
 template <int D, bool QK_MX, int P_MODE, int RB, bool BLASST, bool VALPHA>
-__global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd_kernel(const KArgs a) {
+__global__ void __launch_bounds__(kThreads, BLASST ? 1 : 2) attn_fwd_kernel(const KArgs a) {
   constexpr int NH = D / 64;          // 64-wide contraction halves of D
   constexpr int NDB = D / 32;         // 32-row blocks of O^T
   constexpr int CPT = kTN * D / 16 / kThreads;  // 16-byte chunks per thread per K (and V) tile
@@ -407,15 +407,19 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
   float sigma = 1.0f;  // acc holds O^T / sigma
   float skipped = 0.0f, total = 0.0f;
   v16f acc[NDB];
-  v16f cacc[VALPHA ? NDB : 1];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.0f;
+  // V smoothing (attention_triton.py c = c * alpha + rowsum(P_deq) (x) alpha_v)
+  // is folded into acc: the correction of a tile, rowsum(P_deq) / sigma (x)
+  // alpha_v, is added in the same units as the tile's PV product, so the
+  // accumulator rescale applies to both.  rowsum(codes) comes from one FP8
+  // MFMA of the codes against a constant A = 1.0 (exact in fp32).
+  v8i ones;
 #pragma unroll
-  for (int db = 0; db < (VALPHA ? NDB : 1); ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) cacc[db][r] = 0.0f;
+  for (int q = 0; q < 8; ++q) ones[q] = 0x38383838;  // E4M3 1.0
+  float vw_prev = 0.0f;  // s_P / sigma of tile it-1 (weight of its correction)
 
   // ---- tile loader ------------------------------------------------------------
   // K codes, the qm bias rows and the MX K scales are staged three tiles ahead
@@ -602,6 +606,7 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     uint4* z = reinterpret_cast<uint4*>(&v_lds[3][0]);
     for (int i = tid; i < D * kTN / 16; i += kThreads) z[i] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < kTN) vmeta[3].ve[tid] = 0x7f7f7f7fu;
+    if (VALPHA && tid < D) vmeta[3].valpha[tid] = 0.0f;
   }
   lds_publish<0>();
   v16f sc[2];
@@ -776,6 +781,7 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     const bool clamp = P_MODE == 0 && (HAS_EST || a.p_max_offset > 8);
     float ps4[4];
     v16f bi1;
+    v16f rsm;  // V smoothing: rowsum of the codes of tile it-1
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       __builtin_amdgcn_sched_barrier(0);
@@ -788,6 +794,10 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
         pin(vac);
         if (c + 1 < NDB) va[(c + 1) & 1] = pv_read(vprev, c + 1);
         pv_mfma(c, vac, pop_prev, pe_prev, ve_p[c]);
+      }
+      if (VALPHA && c == 1) {  // row sums of the codes of tile it-1 (every register holds the lane's)
+        const v16f zero = {};
+        rsm = mfma32<false>(ones, pop_prev, zero, 0, 0);
       }
       if (c >= 2 && c - 2 < NH) {
         v8i kac = ka[(c - 2) & 1];
@@ -839,23 +849,17 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     l = l * alpha + psum;
 #undef sv
 
-    // ---- V-smoothing accumulator: c = c * alpha + rowsum(P_deq) (x) alpha_v -------
-    const VMeta<D>& vm = vmeta[vcur];
+    // ---- V smoothing: correction of tile it-1, in the units of its PV product
+    // (added in this step), before this step's rescale ----------------------------
     if constexpr (VALPHA) {
-      float cs = 0.0f;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int wd = pop[q];
-        cs += __builtin_amdgcn_cvt_f32_fp8(wd, 0) + __builtin_amdgcn_cvt_f32_fp8(wd, 1) +
-              __builtin_amdgcn_cvt_f32_fp8(wd, 2) + __builtin_amdgcn_cvt_f32_fp8(wd, 3);
-      }
-      const float rs = xor32_add(cs) * s_lp;
+      const float w = rsm[0] * vw_prev;
+      const VMeta<D>& vmp = vmeta[vprev];
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int d = 32 * db + 8 * (r >> 2) + 4 * g + (r & 3);
-          cacc[db][r] = fmaf(rs, vm.valpha[d], cacc[db][r] * alpha);
+          acc[db][r] = fmaf(w, vmp.valpha[d], acc[db][r]);
         }
     }
 
@@ -863,8 +867,10 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     // scale): the PV of tile it, issued in the next step, accumulates on top ------
     float sig_new = sig_p;
     sig_new *= v_blk ? vsc : 1.0f;
-    const float f = alpha * sigma * __builtin_amdgcn_rcpf(sig_new);
+    const float rsig = __builtin_amdgcn_rcpf(sig_new);
+    const float f = alpha * sigma * rsig;
     sigma = sig_new;
+    if constexpr (VALPHA) vw_prev = s_lp * rsig;  // rowsum(P_deq) / sigma per code unit
     if (P_MODE == 2 || __any(f != 1.0f)) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -906,6 +912,18 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
     const int vl = (nt - 1) & 3;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) pv_mfma(db, pv_read(vl, db), pop_prev, pe_prev, pv_scale(vl, db));
+    if constexpr (VALPHA) {  // correction of the last tile
+      const v16f zero = {};
+      const v16f rl = mfma32<false>(ones, pop_prev, zero, 0, 0);
+      const float w = rl[0] * vw_prev;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int d = 32 * db + 8 * (r >> 2) + 4 * g + (r & 3);
+          acc[db][r] = fmaf(w, vmeta[vl].valpha[d], acc[db][r]);
+        }
+    }
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
@@ -933,7 +951,6 @@ __global__ void __launch_bounds__(kThreads, (BLASST || VALPHA) ? 1 : 2) attn_fwd
       for (int k = 0; k < 4; ++k) {
         float mainv = acc[db][4 * r4 + k] * sigma;
         if (vch) mainv *= vch[d0 + k];
-        if constexpr (VALPHA) mainv += cacc[db][4 * r4 + k];
         // the reference writes a bf16 BHSD tensor, then casts to the output dtype
         o[k] = bf16_bits_to_f32(f32_to_bf16_bits(mainv * inv_l));
       }

@@ -272,7 +272,7 @@ class QuantizedOperands:
     v_block: int
     bias: Optional[torch.Tensor]          # (B,H,G,P) qm.K_s * sm_scale * log2(e)
     rowmax: Optional[torch.Tensor]        # (B,H,G) max_n bias (log2 units)
-    v_alpha: Optional[torch.Tensor]       # (B,H,S/vsb,D) fp32
+    v_alpha: Optional[torch.Tensor]       # (B,H,S/vsb,D) fp32 block means (/ channel V scale)
     out_row_map: Optional[torch.Tensor]   # (B*H,S) int32
 
 
@@ -309,6 +309,10 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
     v_alpha = None
     if prep.v_alpha is not None:
         v_alpha = prep.v_alpha.permute(0, 2, 1, 3).contiguous()
+        if v_kind == 0:
+            # the kernel adds the V-smoothing correction into its accumulator,
+            # which the per-channel V scales multiply at the end
+            v_alpha = v_alpha / v_scale[:, :, None, :]
     return QuantizedOperands(b=b, s=s, h=h, d=d, P=P, q_codes=q_codes, q_scale=q_scale, k_codes=k_codes,
                              k_scale=k_scale, v_codes_t=v_codes, v_scale=v_scale, v_kind=v_kind, v_block=v_block,
                              bias=bias, rowmax=rowmax, v_alpha=v_alpha, out_row_map=prep.q_order_i32())

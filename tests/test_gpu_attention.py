@@ -87,6 +87,9 @@ CASES = {
     "fp8blockV_elementwise_vsmooth": dict(qk_quant="fp8_block", fp8_block_size=64, v_quant="fp8_block",
                                           v_fp8_block_size=64, smoothing="off", q_kmeans_k=None,
                                           v_smooth_mode="per_block", v_smooth_block_size=128),
+    "channelV_dynamic_vsmooth": dict(qk_quant="fp8_block", fp8_block_size=64, v_quant="fp8_channel",
+                                     smoothing="full", q_smooth_block_size=256, q_kmeans_k=None,
+                                     p_quant="dynamic", v_smooth_mode="per_block", v_smooth_block_size=64),
     "default_config": dict(),
 }
 
