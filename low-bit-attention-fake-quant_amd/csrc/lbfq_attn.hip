@@ -132,9 +132,10 @@ extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t strea
   const bool mx = p->qk_mx != 0;
   const int D = static_cast<int>(p->D);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (p->p_mode == 0) return launch_p0(a, D, mx, rb, blasst, valpha, st);
-  if (p->p_mode == 1) return launch_p1(a, D, mx, rb, blasst, valpha, st);
-  return launch_p2(a, D, mx, rb, blasst, valpha, st);
+  const int bl = blasst ? (p->blasst_fill == FILL_UTA ? 2 : 1) : 0;
+  if (p->p_mode == 0) return launch_p0(a, D, mx, rb, bl, valpha, st);
+  if (p->p_mode == 1) return launch_p1(a, D, mx, rb, bl, valpha, st);
+  return launch_p2(a, D, mx, rb, bl, valpha, st);
 }
 
 extern "C" int lbfq_selftest_cvt_fp8(const float* x, int64_t n, uint8_t* out, lbfq_stream_t stream) {

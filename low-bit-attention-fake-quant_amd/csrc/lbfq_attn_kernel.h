@@ -279,6 +279,50 @@ __device__ __forceinline__ float uta_fill(const float (&u)[32], float m_new, flo
   return xor32_max(fmx);
 }
 
+// Fills with one value per row and tile (zero, max, mean, logn, sample8, thr):
+// the value f of the row's valid keys (the keys of a full tile are all valid),
+// computed from the scores in place (u = score * C), as blasst_fill does.
+template <int P_MODE>
+__device__ __forceinline__ float blasst_row_fill(const KArgs& a, const v16f (&sc)[2], const float (&Ct)[2],
+                                                 float m_new, float bmax, float off, int key0) {
+  const int fk = a.fill_kind;
+  const float fa = a.fill_alpha;
+  const int nv = a.S - key0 < kTN ? a.S - key0 : kTN;  // valid keys of the row (uniform)
+  const float n = static_cast<float>(nv), rn = 1.0f / n;
+  const float max_bound = n * fast_exp2(bmax - m_new + off);
+  float f = 0.0f;  // FILL_ZERO
+  if (fk == FILL_MAX) {
+    f = max_bound * fa * rn;
+  } else if (fk == FILL_MEAN || fk == FILL_LOGN) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) s += valid_or(sc[j >> 4][j & 15] * Ct[j >> 4], 0.0f);
+    const float mean = xor32_add(s) * rn;  // log2 units
+    if (fk == FILL_MEAN) {
+      f = fminf(fa * n * fast_exp2(mean - m_new + off), max_bound) * rn;
+    } else {
+      float vs = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const float c = valid_or(sc[j >> 4][j & 15] * Ct[j >> 4] - mean, 0.0f);
+        vs = fmaf(c, c, vs);
+      }
+      const float var2 = xor32_add(vs) * rn;  // log2 units squared
+      f = fminf(n * fast_exp2(mean + 0.5f * var2 * kLn2 - m_new + off), max_bound) * rn;
+    }
+  } else if (fk == FILL_SAMPLE8) {
+    const float c0 = off - m_new;
+    const float sp = xor32_add(fast_exp2(sc[0][0] * Ct[0] + c0) + fast_exp2(sc[0][8] * Ct[0] + c0) +
+                               fast_exp2(sc[1][0] * Ct[1] + c0) + fast_exp2(sc[1][8] * Ct[1] + c0));
+    const float cnt = static_cast<float>((nv + 7) / 8);
+    f = fminf(fa * n * sp / cnt, max_bound) * rn;
+  } else if (fk == FILL_THR) {
+    const float offs = P_MODE == 0 ? exp2f(static_cast<float>(a.p_max_offset)) : 1.0f;
+    f = fa * n * a.lam * offs * rn;
+  }
+  return f;
+}
+
 template <int P_MODE>
 __device__ __forceinline__ float blasst_fill(const KArgs& a, const float (&u)[32], float m_new, float bmax, float off,
                                              int key0, float (&fp)[32]) {
@@ -334,8 +378,12 @@ __device__ __forceinline__ float blasst_fill(const KArgs& a, const float (&u)[32
   return f;
 }
 
-template <int D, bool QK_MX, int P_MODE, int RB, bool BLASST, bool VALPHA>
-__global__ void __launch_bounds__(kThreads, BLASST ? 1 : 2) attn_fwd_kernel(const KArgs a) {
+// BL: BLASST off (0), with a fill of one value per row and tile (1), with the
+// UTA fill of one value per key bin (2; its per-key fill codes take 32
+// registers, so it runs one wave per SIMD).
+template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA>
+__global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(const KArgs a) {
+  constexpr bool BLASST = BL != 0;
   constexpr int NH = D / 64;          // 64-wide contraction halves of D
   constexpr int NDB = D / 32;         // 32-row blocks of O^T
   constexpr int CPT = kTN * D / 16 / kThreads;  // 16-byte chunks per thread per K (and V) tile
@@ -638,9 +686,9 @@ __global__ void __launch_bounds__(kThreads, BLASST ? 1 : 2) attn_fwd_kernel(cons
   int slot = 0;       // K slot of tile it (tile i in slot i % 3); V^T slot: tile i in slot i % 4
   v8i pop_prev;       // P codes of tile it-1 (zero codes before the first tile)
   int pe_prev = 127;  // their E8M0 scale (MX P)
-  float fcq[BLASST ? 32 : 1];  // BLASST: fill codes of the lane's keys (current where the row skips)
+  float fcq[BL == 2 ? 32 : 1];  // UTA fill: fill codes of the lane's keys (current where the row skips)
 #pragma unroll
-  for (int j = 0; j < (BLASST ? 32 : 1); ++j) fcq[j] = 0.0f;
+  for (int j = 0; j < (BL == 2 ? 32 : 1); ++j) fcq[j] = 0.0f;
 #pragma unroll
   for (int q = 0; q < 8; ++q) pop_prev[q] = 0;
   // MASKED: the tile holds keys >= S (only the last tile, when S % 64 != 0);
@@ -734,16 +782,20 @@ __global__ void __launch_bounds__(kThreads, BLASST ? 1 : 2) attn_fwd_kernel(cons
       alpha = fast_exp2(m2 - m_new);
     }
     // BLASST fills of the skipped rows, in p units, and the largest fill of the row
-    float fp[BLASST ? 32 : 1];
+    float fp[BL == 2 ? 32 : 1];
     float fmax = 0.0f;
     bool any_skip = false;
     if constexpr (BLASST) {
       any_skip = __any(skip);
       if (any_skip) {
-        float u[32];
+        if constexpr (BL == 2) {
+          float u[32];
 #pragma unroll
-        for (int j = 0; j < 32; ++j) u[j] = sv(j) * Ct[j >> 4];
-        fmax = blasst_fill<P_MODE>(a, u, m_new, bmax, off, key0, fp);
+          for (int j = 0; j < 32; ++j) u[j] = sv(j) * Ct[j >> 4];
+          fmax = blasst_fill<P_MODE>(a, u, m_new, bmax, off, key0, fp);
+        } else {
+          fmax = blasst_row_fill<P_MODE>(a, sc, Ct, m_new, bmax, off, key0);
+        }
       }
     }
     // P scale of the row (attention_triton.py:330-370): exact rows from the tile
@@ -769,12 +821,16 @@ __global__ void __launch_bounds__(kThreads, BLASST ? 1 : 2) attn_fwd_kernel(cons
       sig_p = s_lp;
       if constexpr (BLASST) qmul_f = kFp8Max / rf;
     }
-    if constexpr (BLASST) {
+    float fq = 0.0f;  // row fill (BL 1) in code units
+    if constexpr (BL == 2) {
       if (any_skip) {
 #pragma unroll
         for (int j = 0; j < 32; ++j) fcq[j] = P_MODE == 0 ? fminf(fp[j], kFp8Max) : fp[j] * qmul_f;
       }
+    } else if constexpr (BL == 1) {
+      fq = P_MODE == 0 ? fminf(fmax, kFp8Max) : fmax * qmul_f;
     }
+    (void)fq;
     (void)qmul_f;
     (void)fp;
     // p may exceed 448 only against an estimated or offset row max: satfinite cast
@@ -814,7 +870,9 @@ __global__ void __launch_bounds__(kThreads, BLASST ? 1 : 2) attn_fwd_kernel(cons
       for (int jj = 0; jj < 8; ++jj) {
         const int j = 8 * c + jj;
         pq[jj] = fast_exp2(fmaf(sv(j), Ct[j >> 4], -Tc));
-        if constexpr (BLASST) pq[jj] = skip ? fcq[j] : pq[jj];  // fill codes of a skipped row
+        // fill codes of a skipped row (zero on the keys past S of the last tile)
+        if constexpr (BL == 2) pq[jj] = skip ? fcq[j] : pq[jj];
+        if constexpr (BL == 1) pq[jj] = skip ? ((MASKED && sv(j) == -INFINITY) ? 0.0f : fq) : pq[jj];
         ps4[j & 3] = j < 4 ? pq[jj] : ps4[j & 3] + pq[jj];
       }
       if constexpr (P_MODE == 0) {
@@ -972,12 +1030,13 @@ __global__ void __launch_bounds__(kThreads, BLASST ? 1 : 2) attn_fwd_kernel(cons
 }
 
 // Launch one instantiation (defined in the per-P-mode translation units).
-int launch_p0(const KArgs& a, int D, bool qk_mx, int rb, bool blasst, bool valpha, hipStream_t st);
-int launch_p1(const KArgs& a, int D, bool qk_mx, int rb, bool blasst, bool valpha, hipStream_t st);
-int launch_p2(const KArgs& a, int D, bool qk_mx, int rb, bool blasst, bool valpha, hipStream_t st);
+// bl: 0 no BLASST, 1 BLASST with a per-row fill, 2 BLASST with the UTA fill.
+int launch_p0(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
+int launch_p1(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
+int launch_p2(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
 
 template <int P_MODE>
-int launch_p(const KArgs& a, int D, bool qk_mx, int rb, bool blasst, bool valpha, hipStream_t st) {
+int launch_p(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st) {
   const int nblk = a.B * a.H * a.nqb;
   dim3 grid(static_cast<unsigned>(nblk)), block(kThreads);
 #define LBFQ_L(DD, MX, RBV, BL, VA) \
@@ -985,7 +1044,7 @@ int launch_p(const KArgs& a, int D, bool qk_mx, int rb, bool blasst, bool valpha
 #define LBFQ_VA(DD, MX, RBV, BL) \
   if (valpha) LBFQ_L(DD, MX, RBV, BL, true); else LBFQ_L(DD, MX, RBV, BL, false)
 #define LBFQ_BL(DD, MX, RBV) \
-  if (blasst) { LBFQ_VA(DD, MX, RBV, true); } else { LBFQ_VA(DD, MX, RBV, false); }
+  if (bl == 2) { LBFQ_VA(DD, MX, RBV, 2); } else if (bl == 1) { LBFQ_VA(DD, MX, RBV, 1); } else { LBFQ_VA(DD, MX, RBV, 0); }
 #define LBFQ_RB(DD, MX)                    \
   if (rb == RB_ONLINE) { LBFQ_BL(DD, MX, RB_ONLINE) }            \
   else if (rb == RB_ONLINE_BIAS) { LBFQ_BL(DD, MX, RB_ONLINE_BIAS) } \

@@ -3,7 +3,7 @@
 #include "lbfq_attn_kernel.h"
 
 namespace lbfq_attn {
-int launch_p2(const KArgs& a, int D, bool qk_mx, int rb, bool blasst, bool valpha, hipStream_t st) {
-  return launch_p<2>(a, D, qk_mx, rb, blasst, valpha, st);
+int launch_p2(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st) {
+  return launch_p<2>(a, D, qk_mx, rb, bl, valpha, st);
 }
 }  // namespace lbfq_attn
