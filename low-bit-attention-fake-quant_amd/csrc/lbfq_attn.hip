@@ -132,7 +132,7 @@ extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t strea
   const bool mx = p->qk_mx != 0;
   const int D = static_cast<int>(p->D);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int bl = blasst ? (p->blasst_fill == FILL_UTA ? 2 : 1) : 0;
+  const int bl = !blasst ? 0 : p->blasst_fill != FILL_UTA ? 1 : (p->blasst_uta_bins <= 16 ? 2 : 3);
   if (p->p_mode == 0) return launch_p0(a, D, mx, rb, bl, valpha, st);
   if (p->p_mode == 1) return launch_p1(a, D, mx, rb, bl, valpha, st);
   return launch_p2(a, D, mx, rb, bl, valpha, st);

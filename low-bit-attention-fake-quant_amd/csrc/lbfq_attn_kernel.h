@@ -323,6 +323,71 @@ __device__ __forceinline__ float blasst_row_fill(const KArgs& a, const v16f (&sc
   return f;
 }
 
+// UTA fill with at most 16 bins (runs of >= 4 keys, at most 8 per lane):
+// uta_runs computes the fill of each of the lane's runs (the arithmetic of
+// uta_fill, with the scores read in place) and returns the row's largest;
+// uta_pack turns them into the lane's E4M3 fill codes, 4 keys per word in the
+// order of the P codes, and their sum in the order of the exact row sum.
+template <int BS>
+__device__ __forceinline__ float uta_runs(const v16f (&sc)[2], const float (&Ct)[2], float m_new, float off,
+                                          float fa, float (&fr)[8]) {
+  constexpr int RUN = BS <= 16 ? BS : 16;
+  constexpr int NR = 32 / RUN;
+  static_assert(NR <= 8, "uta_runs: at most 8 runs per lane");
+  float s[NR], mx[NR], c[NR];
+#pragma unroll
+  for (int b = 0; b < NR; ++b) {
+    s[b] = 0.0f; mx[b] = -INFINITY; c[b] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RUN; ++r) {
+      const int j = RUN * b + r;
+      const float x = sc[j >> 4][j & 15] * Ct[j >> 4];
+      s[b] += valid_or(x, 0.0f);
+      mx[b] = hmax(mx[b], x);
+      c[b] += x != -INFINITY ? 1.0f : 0.0f;
+    }
+    if constexpr (BS >= 32) {
+      s[b] = xor32_add(s[b]);
+      mx[b] = xor32_max(mx[b]);
+      c[b] = xor32_add(c[b]);
+    }
+  }
+  if constexpr (BS == 64) {
+    s[0] += s[1]; mx[0] = hmax(mx[0], mx[1]); c[0] += c[1];
+    s[1] = s[0]; mx[1] = mx[0]; c[1] = c[0];
+  }
+  float fmx = 0.0f;
+#pragma unroll
+  for (int b = 0; b < NR; ++b) {
+    const float sc_b = fmaxf(c[b], 1.0f), rc = __builtin_amdgcn_rcpf(sc_b);
+    const float f = fminf(fa * sc_b * fast_exp2(s[b] * rc - m_new + off), sc_b * fast_exp2(mx[b] - m_new + off)) * rc;
+    fmx = fmaxf(fmx, f);
+    fr[b] = f;
+  }
+  return xor32_max(fmx);
+}
+
+template <int BS, int P_MODE>
+__device__ __forceinline__ void uta_pack(const v16f (&sc)[2], const float (&fr)[8], float qmul_f, uint32_t (&fpk)[8],
+                                         float& fsum) {
+  constexpr int RUN = BS <= 16 ? BS : 16;
+  float s4[4];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * q + i;
+      const float f = sc[j >> 4][j & 15] != -INFINITY ? fr[j / RUN] : 0.0f;
+      v[i] = P_MODE == 0 ? fminf(f, kFp8Max) : f * qmul_f;
+      s4[i] = q == 0 ? v[i] : s4[i] + v[i];
+    }
+    int wd = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], __float_as_int(v[0]), false);
+    fpk[q] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], wd, true));
+  }
+  fsum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+}
+
 template <int P_MODE>
 __device__ __forceinline__ float blasst_fill(const KArgs& a, const float (&u)[32], float m_new, float bmax, float off,
                                              int key0, float (&fp)[32]) {
@@ -378,11 +443,12 @@ __device__ __forceinline__ float blasst_fill(const KArgs& a, const float (&u)[32
   return f;
 }
 
-// BL: BLASST off (0), with a fill of one value per row and tile (1), with the
-// UTA fill of one value per key bin (2; its per-key fill codes take 32
-// registers, so it runs one wave per SIMD).
+// BL: BLASST off (0); with a fill of one value per row and tile (1); with the
+// UTA fill of at most 16 bins (2: packed fill codes per lane); with the UTA
+// fill of 32 or 64 bins (3: one fill code per key in 32 registers, one wave
+// per SIMD).  BLASST together with V smoothing also runs one wave per SIMD.
 template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA>
-__global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(const KArgs a) {
+__global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1 : 2) attn_fwd_kernel(const KArgs a) {
   constexpr bool BLASST = BL != 0;
   constexpr int NH = D / 64;          // 64-wide contraction halves of D
   constexpr int NDB = D / 32;         // 32-row blocks of O^T
@@ -686,9 +752,13 @@ __global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(con
   int slot = 0;       // K slot of tile it (tile i in slot i % 3); V^T slot: tile i in slot i % 4
   v8i pop_prev;       // P codes of tile it-1 (zero codes before the first tile)
   int pe_prev = 127;  // their E8M0 scale (MX P)
-  float fcq[BL == 2 ? 32 : 1];  // UTA fill: fill codes of the lane's keys (current where the row skips)
+  float fcq[BL == 3 ? 32 : 1];  // UTA fill, 32/64 bins: fill codes of the lane's keys (current where the row skips)
 #pragma unroll
-  for (int j = 0; j < (BL == 2 ? 32 : 1); ++j) fcq[j] = 0.0f;
+  for (int j = 0; j < (BL == 3 ? 32 : 1); ++j) fcq[j] = 0.0f;
+  uint32_t fpk[BL == 2 ? 8 : 1];  // UTA fill, <= 16 bins: packed fill codes (current where the row skips)
+  float fsum = 0.0f;              // and their sum in code units
+#pragma unroll
+  for (int q = 0; q < (BL == 2 ? 8 : 1); ++q) fpk[q] = 0u;
 #pragma unroll
   for (int q = 0; q < 8; ++q) pop_prev[q] = 0;
   // MASKED: the tile holds keys >= S (only the last tile, when S % 64 != 0);
@@ -782,13 +852,22 @@ __global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(con
       alpha = fast_exp2(m2 - m_new);
     }
     // BLASST fills of the skipped rows, in p units, and the largest fill of the row
-    float fp[BL == 2 ? 32 : 1];
+    float fp[BL == 3 ? 32 : 1];
+    float fr[8];  // BL 2: fill of each run of the lane
     float fmax = 0.0f;
     bool any_skip = false;
     if constexpr (BLASST) {
       any_skip = __any(skip);
       if (any_skip) {
         if constexpr (BL == 2) {
+          switch (kTN / a.uta_bins) {
+            case 4: fmax = uta_runs<4>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            case 8: fmax = uta_runs<8>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            case 16: fmax = uta_runs<16>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            case 32: fmax = uta_runs<32>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            default: fmax = uta_runs<64>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+          }
+        } else if constexpr (BL == 3) {
           float u[32];
 #pragma unroll
           for (int j = 0; j < 32; ++j) u[j] = sv(j) * Ct[j >> 4];
@@ -823,6 +902,16 @@ __global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(con
     }
     float fq = 0.0f;  // row fill (BL 1) in code units
     if constexpr (BL == 2) {
+      if (any_skip) {
+        switch (kTN / a.uta_bins) {
+          case 4: uta_pack<4, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
+          case 8: uta_pack<8, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
+          case 16: uta_pack<16, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
+          case 32: uta_pack<32, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
+          default: uta_pack<64, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
+        }
+      }
+    } else if constexpr (BL == 3) {
       if (any_skip) {
 #pragma unroll
         for (int j = 0; j < 32; ++j) fcq[j] = P_MODE == 0 ? fminf(fp[j], kFp8Max) : fp[j] * qmul_f;
@@ -871,7 +960,7 @@ __global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(con
         const int j = 8 * c + jj;
         pq[jj] = fast_exp2(fmaf(sv(j), Ct[j >> 4], -Tc));
         // fill codes of a skipped row (zero on the keys past S of the last tile)
-        if constexpr (BL == 2) pq[jj] = skip ? fcq[j] : pq[jj];
+        if constexpr (BL == 3) pq[jj] = skip ? fcq[j] : pq[jj];
         if constexpr (BL == 1) pq[jj] = skip ? ((MASKED && sv(j) == -INFINITY) ? 0.0f : fq) : pq[jj];
         ps4[j & 3] = j < 4 ? pq[jj] : ps4[j & 3] + pq[jj];
       }
@@ -887,6 +976,7 @@ __global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(con
         // (pq[4 h2], dead after this instruction), so no zeroing is needed
         int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2], pq[4 * h2 + 1], __float_as_int(pq[4 * h2]), false);
         pop[2 * c + h2] = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2 + 2], pq[4 * h2 + 3], wd, true);
+        if constexpr (BL == 2) pop[2 * c + h2] = skip ? static_cast<int>(fpk[2 * c + h2]) : pop[2 * c + h2];
       }
       // score block 0 is consumed: it receives the bias of tile it+1
       if (c == 1) qk_init(sc[0], 0);
@@ -903,6 +993,7 @@ __global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(con
 #pragma unroll
     for (int i = NH + 1; i < NQK; ++i) sc[1] = qk_mfma(i, ka[i & 1], sc[1], ke_n[i]);
     float psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+    if constexpr (BL == 2) psum = skip ? fsum : psum;  // the fill codes' sum
     psum *= s_lp;  // sum of the pre-quant p
     l = l * alpha + psum;
 #undef sv
@@ -1030,7 +1121,8 @@ __global__ void __launch_bounds__(kThreads, BL == 2 ? 1 : 2) attn_fwd_kernel(con
 }
 
 // Launch one instantiation (defined in the per-P-mode translation units).
-// bl: 0 no BLASST, 1 BLASST with a per-row fill, 2 BLASST with the UTA fill.
+// bl: 0 no BLASST; BLASST with a per-row fill (1), the UTA fill of <= 16 bins (2)
+// or of 32 / 64 bins (3).
 int launch_p0(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
 int launch_p1(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
 int launch_p2(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
@@ -1043,8 +1135,9 @@ int launch_p(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hip
   hipLaunchKernelGGL((attn_fwd_kernel<DD, MX, P_MODE, RBV, BL, VA>), grid, block, 0, st, a)
 #define LBFQ_VA(DD, MX, RBV, BL) \
   if (valpha) LBFQ_L(DD, MX, RBV, BL, true); else LBFQ_L(DD, MX, RBV, BL, false)
-#define LBFQ_BL(DD, MX, RBV) \
-  if (bl == 2) { LBFQ_VA(DD, MX, RBV, 2); } else if (bl == 1) { LBFQ_VA(DD, MX, RBV, 1); } else { LBFQ_VA(DD, MX, RBV, 0); }
+#define LBFQ_BL(DD, MX, RBV)                                              \
+  if (bl == 3) { LBFQ_VA(DD, MX, RBV, 3); } else if (bl == 2) { LBFQ_VA(DD, MX, RBV, 2); } \
+  else if (bl == 1) { LBFQ_VA(DD, MX, RBV, 1); } else { LBFQ_VA(DD, MX, RBV, 0); }
 #define LBFQ_RB(DD, MX)                    \
   if (rb == RB_ONLINE) { LBFQ_BL(DD, MX, RB_ONLINE) }            \
   else if (rb == RB_ONLINE_BIAS) { LBFQ_BL(DD, MX, RB_ONLINE_BIAS) } \
