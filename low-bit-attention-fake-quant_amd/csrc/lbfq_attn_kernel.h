@@ -925,6 +925,8 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     // p may exceed 448 only against an estimated or offset row max: satfinite cast
     const bool clamp = P_MODE == 0 && (HAS_EST || a.p_max_offset > 8);
     float ps4[4];
+    // BLASST: every row of the wave skips this (full) tile (wave-uniform)
+    const bool skip_all = (BL == 1 || BL == 2) && !MASKED && __all(skip);
     v16f bi1;
     v16f rsm;  // V smoothing: rowsum of the codes of tile it-1
 #pragma unroll
@@ -953,7 +955,9 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       if (c == 0 && NQK > 1) ka[1] = qk_read(nxt, 1);
       if (c == 0) bias_store(bn);  // bias rows of tile it+1 -> this wave's binit rows
       if (c == 2) qk_init(bi1, 1);  // accumulator init of score block 1 (bias of tile it+1)
-      // VALU work of chunk c: keys 8c .. 8c+7 of the lane
+      // VALU work of chunk c: keys 8c .. 8c+7 of the lane (none when every row
+      // of the wave skips the tile: its codes are the fill codes)
+      if (!skip_all) {
       float pq[8];
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
@@ -978,6 +982,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
         pop[2 * c + h2] = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2 + 2], pq[4 * h2 + 3], wd, true);
         if constexpr (BL == 2) pop[2 * c + h2] = skip ? static_cast<int>(fpk[2 * c + h2]) : pop[2 * c + h2];
       }
+      }
       // score block 0 is consumed: it receives the bias of tile it+1
       if (c == 1) qk_init(sc[0], 0);
       use(pop[2 * c]);
@@ -988,6 +993,26 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       if (c >= 2 && c - 2 < NH) use(sc[0]);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (BL == 1 || BL == 2) {
+      if (skip_all) {  // the codes (and for BL 1 the row sum terms) of the fill, as the chunks form them
+        if constexpr (BL == 1) {
+          int wd = __builtin_amdgcn_cvt_pk_fp8_f32(fq, fq, __float_as_int(fq), false);
+          wd = __builtin_amdgcn_cvt_pk_fp8_f32(fq, fq, wd, true);
+          float s8 = fq;
+#pragma unroll
+          for (int i = 1; i < 8; ++i) s8 += fq;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) pop[q] = wd;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) ps4[k] = s8;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) pop[q] = static_cast<int>(fpk[q]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) ps4[k] = 0.0f;  // the row sum is fsum
+        }
+      }
+    }
     // score block 1 is consumed: QK MFMAs of tile it+1 from the bias init
     sc[1] = qk_mfma(NH, ka[NH & 1], bi1, ke_n[NH]);
 #pragma unroll
