@@ -90,6 +90,9 @@ CASES = {
     "channelV_dynamic_vsmooth": dict(qk_quant="fp8_block", fp8_block_size=64, v_quant="fp8_channel",
                                      smoothing="full", q_smooth_block_size=256, q_kmeans_k=None,
                                      p_quant="dynamic", v_smooth_mode="per_block", v_smooth_block_size=64),
+    "blasst_mean_vsmooth": dict(qk_quant="fp8_block", fp8_block_size=64, v_quant="fp8_block", v_fp8_block_size=64,
+                                smoothing="off", q_kmeans_k=None, p_quant="elementwise", v_smooth_mode="per_block",
+                                v_smooth_block_size=64, blasst_lambda=0.05, blasst_fill="mean_a1.5"),
     "default_config": dict(),
 }
 
