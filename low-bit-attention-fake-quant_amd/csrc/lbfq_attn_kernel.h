@@ -519,7 +519,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   float l = 0.0f;  // partial row sum of the pre-quant p over this lane's keys
   float max_seen = -INFINITY;
   float sigma = 1.0f;  // acc holds O^T / sigma
-  float skipped = 0.0f, total = 0.0f;
+  float skipped = 0.0f;  // BLASST: tiles this row skipped
   v16f acc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
@@ -832,7 +832,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       skip = qvalid && (bmax - mij) < a.log2_lam;
       alpha = skip ? 1.0f : fast_exp2(m2 - mij);
       m_new = skip ? m2 : mij;
-      if (g == 0) { skipped += skip ? 1.0f : 0.0f; total += qvalid ? 1.0f : 0.0f; }
+      skipped += skip ? 1.0f : 0.0f;  // branch-free; the g == 0 lanes' counts are written
     } else if constexpr (HAS_EST && P_MODE == 2) {
       // branch-free: without dyn_est, m2 stays at the estimate (adjust is false)
       const bool lzero = xor32_add(l) == 0.0f;  // l >= 0 in both halves
@@ -1107,7 +1107,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     if (a.stats && g == 0 && qvalid) {
       const int rb = qi / a.block_m;
       atomicAdd(a.stats + (static_cast<size_t>(rb) * (a.B * a.H) + bh) * 2 + 0, skipped);
-      atomicAdd(a.stats + (static_cast<size_t>(rb) * (a.B * a.H) + bh) * 2 + 1, total);
+      atomicAdd(a.stats + (static_cast<size_t>(rb) * (a.B * a.H) + bh) * 2 + 1, static_cast<float>(nt));  // tiles seen
     }
   }
   if (!qvalid) return;
