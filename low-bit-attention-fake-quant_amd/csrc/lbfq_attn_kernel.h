@@ -885,7 +885,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       s_lp = 1.0f;
     } else if constexpr (P_MODE == 1) {
       const float ra = fmaxf(skip ? fmax : fast_exp2(bmax - m_new), kAmaxFloor);
-      int e = ceil_log2_exact(ra / kFp8Max);
+      int e = ceil_log2_div448(ra);  // == ceil_log2_exact(ra / 448)
       e = e < -127 ? -127 : (e > 127 ? 127 : e);
       T = m_new + static_cast<float>(e);
       s_lp = __uint_as_float(static_cast<uint32_t>(e + 127) << 23);

@@ -136,6 +136,17 @@ __device__ __forceinline__ int ceil_log2_exact(float r) {
   return e + ((u & 0x7fffffu) != 0u ? 1 : 0);
 }
 
+// ceil(log2(r / 448)) for positive normal fp32 r, with the quotient rounded
+// as an IEEE fp32 division would round it, from r's bits: 448 = 1.75 * 2^8,
+// so with r = (1 + f) 2^E the quotient lies in (2^(E-9), 2^(E-8)] when
+// 1 + f <= 1.75 and in (2^(E-8), 2^(E-7)) otherwise; a quotient within half
+// an ulp of a power of two only arises from 1 + f = 1.75 exactly (then it is
+// that power) or from the float next to it (then it rounds away from it).
+__device__ __forceinline__ int ceil_log2_div448(float r) {
+  const uint32_t u = __float_as_uint(r);
+  return static_cast<int>(u >> 23) - 127 - 8 + ((u & 0x7fffffu) > 0x600000u ? 1 : 0);
+}
+
 // Power-of-two MX scale 2^clamp(ceil(log2(amax/448)), -127, 127) as fp32.
 __device__ __forceinline__ float mx_scale_from_amax(float amax) {
   float r = amax / kFp8Max;
