@@ -282,13 +282,14 @@ __device__ __forceinline__ float uta_fill(const float (&u)[32], float m_new, flo
 // Fills with one value per row and tile (zero, max, mean, logn, sample8, thr):
 // the value f of the row's valid keys (the keys of a full tile are all valid),
 // computed from the scores in place (u = score * C), as blasst_fill does.
-template <int P_MODE>
+template <int P_MODE, bool MASKED>
 __device__ __forceinline__ float blasst_row_fill(const KArgs& a, const v16f (&sc)[2], const float (&Ct)[2],
                                                  float m_new, float bmax, float off, int key0) {
   const int fk = a.fill_kind;
   const float fa = a.fill_alpha;
-  const int nv = a.S - key0 < kTN ? a.S - key0 : kTN;  // valid keys of the row (uniform)
-  const float n = static_cast<float>(nv), rn = 1.0f / n;
+  // valid keys of the row (uniform): a full tile's 64 (1/64 is exact), fewer only in the masked last tile
+  const int nv = MASKED ? (a.S - key0 < kTN ? a.S - key0 : kTN) : kTN;
+  const float n = static_cast<float>(nv), rn = MASKED ? 1.0f / n : 1.0f / kTN;
   const float max_bound = n * fast_exp2(bmax - m_new + off);
   float f = 0.0f;  // FILL_ZERO
   if (fk == FILL_MAX) {
@@ -873,7 +874,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
           for (int j = 0; j < 32; ++j) u[j] = sv(j) * Ct[j >> 4];
           fmax = blasst_fill<P_MODE>(a, u, m_new, bmax, off, key0, fp);
         } else {
-          fmax = blasst_row_fill<P_MODE>(a, sc, Ct, m_new, bmax, off, key0);
+          fmax = blasst_row_fill<P_MODE, MASKED>(a, sc, Ct, m_new, bmax, off, key0);
         }
       }
     }
