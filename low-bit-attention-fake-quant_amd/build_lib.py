@@ -44,8 +44,10 @@ UNITS = {
 def _compile(unit: str, extra: list[str]) -> str:
     src = os.path.join(CSRC, unit)
     obj = os.path.join(BUILD, unit.replace(".hip", ".o"))
-    cmd = COMMON + extra + ["-c", src, "-o", obj]
-    r = subprocess.run(cmd, capture_output=True, text=True)
+    # -save-temps (run inside _build) keeps the device assembly, which the
+    # inline-asm hazard check reads
+    cmd = COMMON + extra + ["-save-temps", "-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True, cwd=BUILD)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {unit}:\n{' '.join(cmd)}\n{r.stderr}")
     return obj
@@ -55,13 +57,29 @@ def _check_mfma(objs: list[str]) -> None:
     sys.path.insert(0, HERE)
     import mfma_check
     if not mfma_check.tools_available():
-        print("mfma_check: ROCm LLVM tools not found; scale-operand check skipped", file=sys.stderr)
+        print("mfma_check: ROCm LLVM tools not found; code checks skipped", file=sys.stderr)
         return
-    bad = {o: mfma_check.check_object(o) for o in objs}
-    bad = {o: b for o, b in bad.items() if b}
+    bad = {}
+    for o in objs:
+        found = mfma_check.check_object(o)
+        s_path = device_asm(o)
+        if os.path.exists(s_path):
+            found += mfma_check.check_assembly(s_path)
+        else:
+            found.append(f"device assembly {os.path.basename(s_path)} missing (inline-asm hazard check not run)")
+        if found:
+            bad[o] = found
     if bad:
         lines = "\n".join(f"{os.path.basename(o)}: {x}" for o, b in bad.items() for x in b[:4])
-        raise RuntimeError("scaled MFMA reads a scale operand from its own destination registers:\n" + lines)
+        raise RuntimeError("gfx950 code check failed (a scaled MFMA reading a scale from its own destination "
+                           "registers, an LDS DMA directly after an M0 write, or inline asm touching an MFMA's "
+                           "registers inside its hazard window):\n" + lines)
+
+
+def device_asm(obj: str) -> str:
+    """Device assembly that -save-temps left next to a unit's object."""
+    base = os.path.basename(obj)[:-2]
+    return os.path.join(os.path.dirname(obj), f"{base}-hip-amdgcn-amd-amdhsa-{ARCH}.s")
 
 
 def build(verbose: bool = True) -> str:

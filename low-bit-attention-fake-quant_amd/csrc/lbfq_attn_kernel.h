@@ -119,20 +119,16 @@ struct VMeta {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Hardware max of raw scores.  fmaxf on a value the compiler cannot prove
-// canonical (an MFMA result, a lane exchange, a loop-carried value) costs an
-// extra v_max x, x, x each; the scores here are finite or -inf, for which the
-// plain instructions are exact.
-__device__ __forceinline__ float hmax3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-__device__ __forceinline__ float hmax(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
+// Max of raw scores (v_max3_f32 / v_max_f32).  These must stay visible to the
+// compiler: the scores are MFMA results, and on gfx950 a VALU instruction may
+// read the destination of a 16-pass XDL MFMA only 20 wait states after it
+// issues.  The compiler inserts those wait states for its own instructions but
+// never inspects the operands that inline asm reads, so a max written as asm
+// can read a partly written accumulator (a wrong row max, then inf / NaN
+// rows, depending on timing).  With this compiler fmaxf needs no
+// canonicalisation of MFMA results, lane exchanges or loop-carried values.
+__device__ __forceinline__ float hmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+__device__ __forceinline__ float hmax(float a, float b) { return fmaxf(a, b); }
 
 template <bool SCALED>
 __device__ __forceinline__ v16f mfma32(const v8i& a, const v8i& b, const v16f& c, int sa, int sb) {
@@ -159,15 +155,23 @@ __device__ __forceinline__ v8i lds_read32(const uint8_t* p0, const uint8_t* p1) 
 // in M0 across these statements.
 // Addressing: wave-uniform 64-bit global base (SGPRs) + per-lane 32-bit byte
 // offset, LDS base as a wave-uniform byte address.
+// On GFX9-family parts (gfx950 included) an LDS DMA that reads M0 right after
+// an SALU write of M0 needs one wait state; the compiler's hazard recognizer
+// cannot see inside inline asm, so each copy carries its own s_nop 0 (else the
+// copy may use the previous M0 and land in the previous copy's LDS slot).
+// build_lib.py rejects any object in which an M0 write directly precedes an
+// LDS DMA.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
 }
 __device__ __forceinline__ void g2l16(const void* gbase, uint32_t vofs, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(vofs), "s"(gbase), "s"(lds_base)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(vofs), "s"(gbase),
+               "s"(lds_base)
                : "memory", "m0");
 }
 __device__ __forceinline__ void g2l4(const void* gbase, uint32_t vofs, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(vofs), "s"(gbase), "s"(lds_base)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(vofs), "s"(gbase),
+               "s"(lds_base)
                : "memory", "m0");
 }
 // Scheduling fences for register values (no instruction is emitted): pin(x)
@@ -1064,7 +1068,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     slot = nxt;
   };
   const int nfull = (S % kTN) ? nt - 1 : nt;
-  if constexpr (!QK_MX) {
+  {
     // two steps per iteration: the loop-carried scores, P codes and ring state
     // alternate between two register sets instead of being copied at the back edge
     int it0 = 0;
@@ -1073,8 +1077,6 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       step(it0 + 1, std::false_type{});
     }
     if (it0 < nfull) step(it0, std::false_type{});
-  } else {
-    for (int it = 0; it < nfull; ++it) step(it, std::false_type{});
   }
   if (nfull < nt) step(nt - 1, std::true_type{});
   if constexpr (QK_MX) {

@@ -1,5 +1,17 @@
-"""Build-time check of the compiled gfx950 code: no ``v_mfma_scale`` may read
-an E8M0 scale operand from a register inside its own destination range.
+"""Build-time checks of the compiled gfx950 code.
+
+1. No ``v_mfma_scale`` may read an E8M0 scale operand from a register inside
+   its own destination range.
+2. No LDS DMA (``global_load_lds_*`` / ``buffer_load_* ... lds``) may directly
+   follow an SALU write of M0: GFX9-family parts need one wait state between
+   the two, and the compiler cannot insert it inside inline asm.
+3. No instruction written as inline asm may read or write the destination of
+   an MFMA within the 20 wait states that follow it (a 16-pass XDL MFMA on
+   gfx950), nor write one of its SrcC registers within 15.  The hardware does
+   not interlock these; the compiler inserts the wait states for its own
+   instructions but does not look at the operands of inline asm.  This check
+   reads the compiler's assembly output (``-save-temps``), where inline asm is
+   bracketed by ``;;#ASMSTART`` / ``;;#ASMEND``.
 
 When the accumulator input of a scaled MFMA is the constant 0, the compiler
 does not tie the destination to it and can allocate the destination over a
@@ -63,5 +75,103 @@ def scale_dst_overlaps(asm: str) -> list:
     return bad
 
 
+def _instructions(asm: str) -> list:
+    """Instruction mnemonics + operands in program order (labels and blanks dropped)."""
+    out = []
+    for line in asm.splitlines():
+        t = line.split("//")[0].strip()
+        if not t or t.endswith(":") or t.startswith(("Disassembly", ".")) or "file format" in t:
+            continue
+        out.append(t)
+    return out
+
+
+def _writes_m0(ins: str) -> bool:
+    parts = ins.split(None, 1)
+    return parts[0].startswith("s_") and len(parts) > 1 and parts[1].split(",")[0].strip() == "m0"
+
+
+def _is_lds_dma(ins: str) -> bool:
+    op = ins.split(None, 1)[0]
+    return op.startswith("global_load_lds") or (op.startswith("buffer_load") and re.search(r"\blds\b", ins) is not None)
+
+
+def m0_lds_dma_hazards(asm: str) -> list:
+    """LDS DMA instructions issued directly after an SALU write of M0."""
+    ins = _instructions(asm)
+    return [f"{ins[i - 1]} ; {ins[i]}" for i in range(1, len(ins)) if _is_lds_dma(ins[i]) and _writes_m0(ins[i - 1])]
+
+
+_REGS = re.compile(r"\b([vsa])(\d+)\b|\b([vsa])\[(\d+):(\d+)\]")
+XDL_READ_WAIT = 20   # wait states before a VALU/VMEM/LDS access of a 16-pass XDL result (gfx950)
+XDL_SRCC_WAR_WAIT = 15
+
+
+def _reg_set(ops: str) -> set:
+    out = set()
+    for m in _REGS.finditer(ops):
+        if m.group(1):
+            out.add((m.group(1), int(m.group(2))))
+        else:
+            out.update((m.group(3), r) for r in range(int(m.group(4)), int(m.group(5)) + 1))
+    return out
+
+
+def _asm_listing(s_text: str) -> list:
+    """(instruction, from_inline_asm) in program order from compiler assembly."""
+    out, in_asm = [], False
+    for line in s_text.splitlines():
+        t = line.strip()
+        if t.startswith(";;#ASMSTART"):
+            in_asm = True
+            continue
+        if t.startswith(";;#ASMEND"):
+            in_asm = False
+            continue
+        t = t.split(";")[0].strip()
+        if not t or t.startswith(".") or t.endswith(":"):
+            continue
+        out.append((t, in_asm))
+    return out
+
+
+def asm_mfma_operand_hazards(s_text: str) -> list:
+    """Inline-asm instructions that touch an MFMA's registers inside its hazard window."""
+    ins = _asm_listing(s_text)
+    bad = []
+    for i, (t, _) in enumerate(ins):
+        if not t.startswith("v_mfma"):
+            continue
+        ops = [o.strip() for o in t.split(None, 1)[1].split(",")]
+        dst = _reg_set(ops[0])
+        srcc = _reg_set(ops[3]) if len(ops) > 3 else set()
+        ws = 0
+        for t2, from_asm in ins[i + 1:]:
+            if t2.startswith("s_nop"):
+                ws += int(t2.split()[1]) + 1
+                continue
+            if t2.startswith(("s_branch", "s_setpc", "s_endpgm")):
+                break
+            ws += 1
+            if ws > XDL_READ_WAIT:
+                break
+            if not from_asm or t2.startswith("v_mfma"):
+                continue
+            parts = t2.split(None, 1)
+            if len(parts) < 2:
+                continue
+            regs = _reg_set(parts[1])
+            d2 = _reg_set(parts[1].split(",")[0])
+            if regs & dst or (ws <= XDL_SRCC_WAR_WAIT and d2 & srcc):
+                bad.append(f"{t} ... {t2} ({ws} issue slots later)")
+    return bad
+
+
+def check_assembly(s_path: str) -> list:
+    with open(s_path) as f:
+        return asm_mfma_operand_hazards(f.read())
+
+
 def check_object(obj: str) -> list:
-    return scale_dst_overlaps(disassemble(obj))
+    asm = disassemble(obj)
+    return scale_dst_overlaps(asm) + m0_lds_dma_hazards(asm)
