@@ -169,9 +169,23 @@ typedef struct {
   float* blasst_stats;            /* (ceil(S/block_m), B*H, 2) fp32, zeroed, or NULL */
   void* out; int out_dtype;       /* NHD (B,S,H,D)                                 */
   const int32_t* out_row_map;     /* (B*H, S): output row of reordered query, or NULL */
+  float* blasst_row_skips;        /* (B*H, S) fp32 in output-row order: K blocks each */
+                                  /* row skipped (the per-row decisions behind the  */
+                                  /* stats, attention_triton.py:165-175), or NULL   */
 } lbfq_attn_params;
 
 int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t stream);
+
+/* Scores of lbfq_attention_fwd's K-loop in log2 units, u = (Q K^T * sm_scale +
+ * the qm correction) * log2(e), formed exactly as the kernel forms them (same
+ * FP8 MFMA operand layout, accumulation order and scale products), for the
+ * query rows `rows` (n_rows indices into the kernel's row order, the same for
+ * every (b, h)): u is (B*H, n_rows, S) fp32.  Uses the Q/K fields of p only.
+ * A diagnostic: it replaces the score part of attention_triton.py:150-162 so
+ * that the reference's softmax / P quantisation can be replayed on the
+ * kernel's own scores. */
+int lbfq_attention_scores(const lbfq_attn_params* p, const int32_t* rows, int64_t n_rows, float* u,
+                          lbfq_stream_t stream);
 
 /* ---- diagnostics -------------------------------------------------------------
  * Replaces p_requant.py:44-73 (p_requant_rows, kernel :12-41).  scores is

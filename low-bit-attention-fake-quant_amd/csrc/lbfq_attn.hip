@@ -56,40 +56,24 @@ __global__ void selftest_mfma_kernel(const uint8_t* A, const uint8_t* Bm, const 
   use(sb);
 }
 
-}  // namespace
-
-extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t stream) {
-  LBFQ_CHECK_ARG(p, "lbfq_attention_fwd: null params");
-  LBFQ_CHECK_ARG(p->D == 64 || p->D == 128, "lbfq_attention_fwd: D must be 64 or 128; got %lld", (long long)p->D);
-  LBFQ_CHECK_ARG(p->B > 0 && p->H > 0 && p->S > 0, "lbfq_attention_fwd: empty shape");
-  LBFQ_CHECK_ARG(p->s_pitch >= p->S && p->s_pitch % kQB == 0,
-                 "lbfq_attention_fwd: s_pitch must be >= S and a multiple of %d", kQB);
+// Argument checks shared by the attention and its score probe; fills the
+// kernel arguments.  Returns 0 or -1 (error message set).
+int make_kargs(const lbfq_attn_params* p, KArgs& a, const char* who) {
+  LBFQ_CHECK_ARG(p, "%s: null params", who);
+  LBFQ_CHECK_ARG(p->D == 64 || p->D == 128, "%s: D must be 64 or 128; got %lld", who, (long long)p->D);
+  LBFQ_CHECK_ARG(p->B > 0 && p->H > 0 && p->S > 0, "%s: empty shape", who);
+  LBFQ_CHECK_ARG(p->s_pitch >= p->S && p->s_pitch % kQB == 0, "%s: s_pitch must be >= S and a multiple of %d", who,
+                 kQB);
   LBFQ_CHECK_ARG(p->s_pitch < (int64_t{1} << 30) && p->B * p->H * (p->s_pitch / kQB) < (int64_t{1} << 31),
-                 "lbfq_attention_fwd: problem too large");
-  LBFQ_CHECK_ARG(p->q_codes && p->k_codes && p->v_codes_t && p->out && p->q_scale && p->k_scale,
-                 "lbfq_attention_fwd: missing tensor");
+                 "%s: problem too large", who);
+  LBFQ_CHECK_ARG(p->q_codes && p->k_codes && p->q_scale && p->k_scale, "%s: missing tensor", who);
   LBFQ_CHECK_ARG(p->qk_mx || (p->qk_block >= 16 && is_pow2(p->qk_block)),
-                 "lbfq_attention_fwd: fp8_block size must be a power of two >= 16; got %d", p->qk_block);
-  LBFQ_CHECK_ARG(p->v_kind >= 0 && p->v_kind <= 2 && p->v_scale, "lbfq_attention_fwd: bad V kind");
-  LBFQ_CHECK_ARG(p->v_kind == 0 || (p->v_block >= kTN && is_pow2(p->v_block) && p->S % p->v_block == 0),
-                 "lbfq_attention_fwd: V block (%d) must be a power of two >= %d dividing S", p->v_block, kTN);
-  LBFQ_CHECK_ARG(p->p_mode >= 0 && p->p_mode <= 2, "lbfq_attention_fwd: bad P mode");
-  LBFQ_CHECK_ARG(!p->rowmax_est || p->qk_bias, "lbfq_attention_fwd: rowmax_est needs the qm correction table");
+                 "%s: fp8_block size must be a power of two >= 16; got %d", who, p->qk_block);
+  LBFQ_CHECK_ARG(!p->rowmax_est || p->qk_bias, "%s: rowmax_est needs the qm correction table", who);
   LBFQ_CHECK_ARG(!p->qk_bias || (p->q_group >= 32 && is_pow2(p->q_group) && p->S % p->q_group == 0),
-                 "lbfq_attention_fwd: q_group must be a power of two >= 32 dividing S");
-  LBFQ_CHECK_ARG(!p->v_alpha || (p->v_smooth_block >= kTN && is_pow2(p->v_smooth_block) &&
-                                  p->S % p->v_smooth_block == 0),
-                 "lbfq_attention_fwd: v_smooth_block must be a power of two >= %d dividing S", kTN);
-  LBFQ_CHECK_ARG(!p->blasst_stats || p->block_m > 0, "lbfq_attention_fwd: block_m must be positive");
-  LBFQ_CHECK_ARG(p->blasst_lambda < 1.0f, "lbfq_attention_fwd: lambda must be < 1");
-  LBFQ_CHECK_ARG(p->blasst_lambda <= 0.0f || p->blasst_fill != FILL_UTA ||
-                     (p->blasst_uta_bins > 0 && kTN % p->blasst_uta_bins == 0),
-                 "lbfq_attention_fwd: UTA bins must divide %d", kTN);
-  LBFQ_CHECK_ARG(p->blasst_fill >= FILL_ZERO && p->blasst_fill <= FILL_UTA, "lbfq_attention_fwd: bad fill kind");
-  LBFQ_CHECK_ARG(p->out_dtype >= 0 && p->out_dtype <= 2, "lbfq_attention_fwd: bad out dtype");
-
+                 "%s: q_group must be a power of two >= 32 dividing S", who);
   const bool blasst = p->blasst_lambda > 0.0f;
-  KArgs a{};
+  a = KArgs{};
   a.B = static_cast<int>(p->B);
   a.H = static_cast<int>(p->H);
   a.S = static_cast<int>(p->S);
@@ -123,10 +107,109 @@ extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t strea
   a.rowmax = p->rowmax_est;
   a.v_alpha = p->v_alpha;
   a.stats = p->blasst_stats;
+  a.row_skips = p->blasst_row_skips;
   a.out = p->out;
   a.out_dtype = p->out_dtype;
   a.out_row_map = p->out_row_map;
+  return 0;
+}
 
+// Scores of the attention K-loop, in log2 units, u = acc * C, for a list of
+// query rows: the same operand bytes in the same MFMA K slots (slot k of the
+// 64-wide half hh holds d = 64 hh + k), the same accumulator start
+// bias * (1/qC * rcp(k scale)), the halves accumulated in the same order and
+// the same score scale C = qC * k scale, so the values are the ones the
+// attention kernel forms (its keys sit in other accumulator rows, which does
+// not change any element's sum).  One wave = 32 rows x 32 keys.
+template <int D, bool QK_MX, bool HAS_BIAS>
+__global__ void __launch_bounds__(64) attn_scores_kernel(const KArgs a, const int32_t* rows, int nrows, float* u) {
+  constexpr int NH = D / 64;
+  const int lane = threadIdx.x, li = lane & 31, g = lane >> 5;
+  const int bh = blockIdx.z;
+  const int ri = blockIdx.y * 32 + li;
+  const int qi = rows[ri < nrows ? ri : nrows - 1];
+  const int kb0 = blockIdx.x * 32;
+  const int S = a.S, P = a.P;
+  v8i qop[NH], kop[NH];
+  int qe[NH], ke[NH];
+  const int key_a = kb0 + li < S ? kb0 + li : S - 1;  // A row li (keys past S are never stored)
+  const uint8_t* qrow = a.q_codes + (static_cast<size_t>(bh) * P + qi) * D;
+  const uint8_t* krow = a.k_codes + (static_cast<size_t>(bh) * P + key_a) * D;
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh) {
+    qop[hh] = lds_read32(qrow + 64 * hh + 16 * g, qrow + 64 * hh + 32 + 16 * g);
+    kop[hh] = lds_read32(krow + 64 * hh + 16 * g, krow + 64 * hh + 32 + 16 * g);
+    qe[hh] = 127;
+    ke[hh] = 127;
+    if constexpr (QK_MX) {
+      qe[hh] = reinterpret_cast<const uint8_t*>(a.q_scale)[(static_cast<size_t>(bh) * P + qi) * (D / 32) + 2 * hh + g];
+      ke[hh] = reinterpret_cast<const uint8_t*>(a.k_scale)[(static_cast<size_t>(bh) * P + key_a) * (D / 32) + 2 * hh + g];
+    }
+  }
+  float qC = a.sml2;
+  if constexpr (!QK_MX) qC *= reinterpret_cast<const float*>(a.q_scale)[bh * a.nqkblk + (qi >> a.lg_qkblk)];
+  const float inv_qC = 1.0f / qC;
+  int grp = 0;
+  if constexpr (HAS_BIAS) {
+    grp = qi >> a.lg_qgroup;
+    if (grp >= a.G) grp = a.G - 1;
+  }
+  auto kscale = [&](int key) -> float {
+    int kb = key >> a.lg_qkblk;
+    kb = kb < a.nqkblk ? kb : a.nqkblk - 1;
+    return reinterpret_cast<const float*>(a.k_scale)[bh * a.nqkblk + kb];
+  };
+  v16f acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    acc[r] = 0.0f;
+    if constexpr (HAS_BIAS) {
+      const int kr = kb0 + 8 * (r >> 2) + 4 * g + (r & 3);
+      const int kc = kr < S ? kr : S - 1;
+      float rr = 1.0f;
+      if constexpr (!QK_MX) rr = __builtin_amdgcn_rcpf(kscale(kc));
+      acc[r] = a.bias[(static_cast<size_t>(bh) * a.G + grp) * P + kc] * (inv_qC * rr);
+    }
+  }
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh) acc = mfma32<QK_MX>(kop[hh], qop[hh], acc, ke[hh], qe[hh]);
+  if (ri >= nrows) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int kr = kb0 + 8 * (r >> 2) + 4 * g + (r & 3);
+    if (kr >= S) continue;
+    const float Ct = QK_MX ? qC : qC * kscale(kr);
+    u[(static_cast<size_t>(bh) * nrows + ri) * S + kr] = acc[r] * Ct;
+  }
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh) {
+    use(qe[hh]);
+    use(ke[hh]);
+  }
+}
+
+}  // namespace
+
+extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t stream) {
+  KArgs a;
+  if (make_kargs(p, a, "lbfq_attention_fwd")) return -1;
+  LBFQ_CHECK_ARG(p->v_codes_t && p->out, "lbfq_attention_fwd: missing tensor");
+  LBFQ_CHECK_ARG(p->v_kind >= 0 && p->v_kind <= 2 && p->v_scale, "lbfq_attention_fwd: bad V kind");
+  LBFQ_CHECK_ARG(p->v_kind == 0 || (p->v_block >= kTN && is_pow2(p->v_block) && p->S % p->v_block == 0),
+                 "lbfq_attention_fwd: V block (%d) must be a power of two >= %d dividing S", p->v_block, kTN);
+  LBFQ_CHECK_ARG(p->p_mode >= 0 && p->p_mode <= 2, "lbfq_attention_fwd: bad P mode");
+  LBFQ_CHECK_ARG(!p->v_alpha || (p->v_smooth_block >= kTN && is_pow2(p->v_smooth_block) &&
+                                  p->S % p->v_smooth_block == 0),
+                 "lbfq_attention_fwd: v_smooth_block must be a power of two >= %d dividing S", kTN);
+  LBFQ_CHECK_ARG(!p->blasst_stats || p->block_m > 0, "lbfq_attention_fwd: block_m must be positive");
+  LBFQ_CHECK_ARG(p->blasst_lambda < 1.0f, "lbfq_attention_fwd: lambda must be < 1");
+  LBFQ_CHECK_ARG(p->blasst_lambda <= 0.0f || p->blasst_fill != FILL_UTA ||
+                     (p->blasst_uta_bins > 0 && kTN % p->blasst_uta_bins == 0),
+                 "lbfq_attention_fwd: UTA bins must divide %d", kTN);
+  LBFQ_CHECK_ARG(p->blasst_fill >= FILL_ZERO && p->blasst_fill <= FILL_UTA, "lbfq_attention_fwd: bad fill kind");
+  LBFQ_CHECK_ARG(p->out_dtype >= 0 && p->out_dtype <= 2, "lbfq_attention_fwd: bad out dtype");
+
+  const bool blasst = p->blasst_lambda > 0.0f;
   const int rb = p->rowmax_est ? RB_EST_BIAS : (p->qk_bias ? RB_ONLINE_BIAS : RB_ONLINE);
   const bool valpha = p->v_alpha != nullptr;
   const bool mx = p->qk_mx != 0;
@@ -136,6 +219,30 @@ extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t strea
   if (p->p_mode == 0) return launch_p0(a, D, mx, rb, bl, valpha, st);
   if (p->p_mode == 1) return launch_p1(a, D, mx, rb, bl, valpha, st);
   return launch_p2(a, D, mx, rb, bl, valpha, st);
+}
+
+extern "C" int lbfq_attention_scores(const lbfq_attn_params* p, const int32_t* rows, int64_t n_rows, float* u,
+                                     lbfq_stream_t stream) {
+  KArgs a;
+  if (make_kargs(p, a, "lbfq_attention_scores")) return -1;
+  LBFQ_CHECK_ARG(rows && u && n_rows > 0 && n_rows < (int64_t{1} << 24), "lbfq_attention_scores: bad row list");
+  dim3 grid(static_cast<unsigned>((p->S + 31) / 32), static_cast<unsigned>((n_rows + 31) / 32),
+            static_cast<unsigned>(p->B * p->H));
+  LBFQ_CHECK_ARG(grid.z <= 65535 && grid.y <= 65535, "lbfq_attention_scores: grid too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nr = static_cast<int>(n_rows);
+  const bool bias = p->qk_bias != nullptr;
+#define LBFQ_SC(DD, MX, BI) hipLaunchKernelGGL((attn_scores_kernel<DD, MX, BI>), grid, dim3(64), 0, st, a, rows, nr, u)
+#define LBFQ_SC_B(DD, MX) \
+  if (bias) { LBFQ_SC(DD, MX, true); } else { LBFQ_SC(DD, MX, false); }
+#define LBFQ_SC_M(DD) \
+  if (p->qk_mx) { LBFQ_SC_B(DD, true) } else { LBFQ_SC_B(DD, false) }
+  if (p->D == 128) { LBFQ_SC_M(128) } else { LBFQ_SC_M(64) }
+#undef LBFQ_SC_M
+#undef LBFQ_SC_B
+#undef LBFQ_SC
+  LBFQ_LAUNCH_CHECK("lbfq_attention_scores");
+  return 0;
 }
 
 extern "C" int lbfq_selftest_cvt_fp8(const float* x, int64_t n, uint8_t* out, lbfq_stream_t stream) {

@@ -97,6 +97,7 @@ struct KArgs {
   const float* rowmax;
   const float* v_alpha;
   float* stats;
+  float* row_skips;
   void* out;
   int out_dtype;
   const int32_t* out_row_map;
@@ -1116,6 +1117,9 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   if (!qvalid) return;
   const float inv_l = 1.0f / lfull;
   const int orow = a.out_row_map ? a.out_row_map[static_cast<size_t>(bh) * S + qi] : qi;
+  if constexpr (BLASST) {
+    if (a.row_skips && g == 0) a.row_skips[static_cast<size_t>(bh) * S + orow] = skipped;
+  }
   const size_t obase = ((static_cast<size_t>(b) * S + orow) * a.H + h) * D;
   const float* vch = a.v_kind == 0 ? reinterpret_cast<const float*>(a.v_scale) + static_cast<size_t>(bh) * D : nullptr;
 #pragma unroll

@@ -80,6 +80,7 @@ class AttnParams(ctypes.Structure):
         ("blasst_stats", _vp),
         ("out", _vp), ("out_dtype", _i32),
         ("out_row_map", _vp),
+        ("blasst_row_skips", _vp),
     ]
 
 
@@ -130,6 +131,7 @@ _SIGS = {
     "lbfq_qmk_kquant": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _vp,
                                _vp, _i64, _vp, _i64, _vp]),
     "lbfq_attention_fwd": (_i32, [ctypes.POINTER(AttnParams), _vp]),
+    "lbfq_attention_scores": (_i32, [ctypes.POINTER(AttnParams), _vp, _i64, _vp, _vp]),
     "lbfq_p_requant_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
                                    ctypes.c_double, _i32, _vp]),
     "lbfq_rowmax_count": (_i32, [ctypes.POINTER(RowmaxCountParams), _vp]),

@@ -145,11 +145,8 @@ def validate_kernel_config(cfg, *, s: int, d: int, has_qm: bool, has_v_alpha: bo
                          f"got {cfg.q_smooth_block_size}")
 
 
-def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, return_blasst_stats: bool = False):
-    """Run the attention kernel on quantised operands; returns NHD output (and stats)."""
-    lib = _lib.load()
-    dev = ops.q_codes.device
-    out = torch.empty((ops.b, ops.s, ops.h, ops.d), dtype=out_dtype, device=dev)
+def _attn_params(ops, cfg, sm_scale: float) -> "_lib.AttnParams":
+    """lbfq_attn_params for the quantised operands (no output, stats or skip buffers)."""
     p = _lib.AttnParams()
     p.B, p.H, p.S, p.D = ops.b, ops.h, ops.s, ops.d
     p.s_pitch = ops.P
@@ -171,26 +168,62 @@ def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, retur
     p.rowmax_dynamic = 1 if p_mode == "dynamic" else 0
     p.v_alpha = _lib.ptr(ops.v_alpha)
     p.v_smooth_block = int(cfg.v_smooth_block_size) if ops.v_alpha is not None else 0
-    stats = None
     if cfg.blasst_lambda is not None:
         kind, alpha, bins = parse_blasst_fill(cfg.blasst_fill, alpha=cfg.blasst_fill_alpha,
                                               uta_bins=cfg.blasst_uta_bins)
         p.blasst_lambda = float(cfg.blasst_lambda)
         p.blasst_fill, p.blasst_fill_alpha, p.blasst_uta_bins = kind, float(alpha), int(bins)
+    else:
+        p.blasst_lambda = 0.0
+        p.blasst_fill, p.blasst_fill_alpha, p.blasst_uta_bins = 0, 1.0, 1
+    p.out_row_map = _lib.ptr(ops.out_row_map)
+    return p
+
+
+def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, return_blasst_stats: bool = False,
+                     return_row_skips: bool = False):
+    """Run the attention kernel on quantised operands; returns NHD output, then
+    (when asked) the BLASST stats (ceil(S/block_m), B*H, 2) and the per-row
+    skipped K-block counts (B*H, S) in output-row order."""
+    lib = _lib.load()
+    dev = ops.q_codes.device
+    out = torch.empty((ops.b, ops.s, ops.h, ops.d), dtype=out_dtype, device=dev)
+    p = _attn_params(ops, cfg, sm_scale)
+    stats = row_skips = None
+    if cfg.blasst_lambda is not None:
         if return_blasst_stats:
             nblk = (ops.s + cfg.p_requant_block_m - 1) // cfg.p_requant_block_m
             stats = torch.zeros((nblk, ops.b * ops.h, 2), dtype=torch.float32, device=dev)
             p.blasst_stats = stats.data_ptr()
-    else:
-        p.blasst_lambda = 0.0
-        p.blasst_fill, p.blasst_fill_alpha, p.blasst_uta_bins = 0, 1.0, 1
+        if return_row_skips:
+            row_skips = torch.zeros((ops.b * ops.h, ops.s), dtype=torch.float32, device=dev)
+            p.blasst_row_skips = row_skips.data_ptr()
     p.out = out.data_ptr()
     p.out_dtype = _lib.DTYPE_CODE[out_dtype]
-    p.out_row_map = _lib.ptr(ops.out_row_map)
     _lib.check(lib.lbfq_attention_fwd(p, _lib.stream_handle(dev)), "lbfq_attention_fwd")
+    res = [out]
     if return_blasst_stats:
-        return out, stats
-    return out
+        res.append(stats)
+    if return_row_skips:
+        res.append(row_skips)
+    return res[0] if len(res) == 1 else tuple(res)
+
+
+def attention_scores(ops, cfg, sm_scale: float, rows: torch.Tensor | None = None) -> torch.Tensor:
+    """The attention kernel's scores in log2 units for the given query rows of
+    its (reordered) row order: (B*H, len(rows), S) fp32 (diagnostic)."""
+    lib = _lib.load()
+    dev = ops.q_codes.device
+    if rows is None:
+        rows = torch.arange(ops.s, device=dev, dtype=torch.int32)
+    rows = rows.to(device=dev, dtype=torch.int32).contiguous()
+    if rows.numel() == 0 or int(rows.min()) < 0 or int(rows.max()) >= ops.s:
+        raise ValueError(f"rows must be non-empty indices in [0, {ops.s})")
+    u = torch.empty((ops.b * ops.h, rows.numel(), ops.s), dtype=torch.float32, device=dev)
+    p = _attn_params(ops, cfg, sm_scale)
+    _lib.check(lib.lbfq_attention_scores(p, rows.data_ptr(), rows.numel(), u.data_ptr(), _lib.stream_handle(dev)),
+               "lbfq_attention_scores")
+    return u
 
 
 def attention_flops(s: int, h: int, d: int, b: int = 1) -> float:
@@ -198,5 +231,5 @@ def attention_flops(s: int, h: int, d: int, b: int = 1) -> float:
     return 4.0 * float(s) * float(s) * float(d) * float(h) * float(b)
 
 
-__all__ = ["parse_blasst_fill", "validate_kernel_config", "launch_attention", "attention_flops",
-           "resolve_p_mode", "math"]
+__all__ = ["parse_blasst_fill", "validate_kernel_config", "launch_attention", "attention_scores",
+           "attention_flops", "resolve_p_mode", "math"]

@@ -100,6 +100,21 @@ def _f32(x: float) -> torch.Tensor:
     return torch.tensor(x, dtype=torch.float32)
 
 
+_E4M3_MAG = np.unique(np.abs(fp8.DECODE[~np.isnan(fp8.DECODE)])).astype(np.float64)   # 0 .. 448, sorted
+EDGE_REL = 2.0 ** -15
+
+
+def rounding_edge_step(x: torch.Tensor, rel: float = EDGE_REL) -> torch.Tensor:
+    """Per element of x (P in code units): the E4M3 step between the two codes
+    around x when |x| lies within rel * |x| of the rounding midpoint between
+    them (a value whose code a relative change of rel can flip), else 0."""
+    a = np.abs(x.double().numpy())
+    i = np.clip(np.searchsorted(_E4M3_MAG, a), 1, len(_E4M3_MAG) - 1)
+    lo, hi = _E4M3_MAG[i - 1], _E4M3_MAG[i]
+    near = (np.abs(a - (lo + hi) / 2) <= rel * a) & (a < 448.0)
+    return torch.from_numpy(np.where(near, hi - lo, 0.0)).float()
+
+
 def estimate_rowmax_qm_k(qm: torch.Tensor, k_work: torch.Tensor, *, block_q: int, sm_scale: float) -> torch.Tensor:
     """``attention.py:366-395``: (B,H,S) fp32 = max_n(qm[g] . K_s[n]) * sm_scale."""
     qm_b = qm.permute(0, 2, 1, 3).float()                 # (B,H,G,D)
@@ -113,7 +128,20 @@ def attention(q, k, v, v_scale, *, sm_scale, p_max_offset, block_m=64, block_n=6
               v_block_scale=None, v_block_size=0, p_quant_mode="elementwise",
               rowmax_est=None, rowmax_init=None, blasst_lambda=None, blasst_fill_mode="zero",
               blasst_fill_alpha=1.0, blasst_uta_bins=16, return_blasst_stats=False,
-              rows=None, return_debug=False):
+              rows=None, return_debug=False, scores_log2=None, force_codes=None):
+    """``scores_log2`` (B,H,R,S), when given, replaces the score computation
+    (q.k * sm_scale + the qm correction, lines 150-162) by supplied scores in
+    log2 units (s = u / log2 e); everything after the scores runs unchanged.
+    ``force_codes`` = (codes (B,H,R,S) uint8, mask (B,H,R,S) bool) replaces the
+    E4M3 P codes at the masked positions before dequantisation.
+    ``return_debug`` adds a dict with the per-block skip masks, the scores
+    ``s`` (B,H,R,S, natural units), the P codes (B,H,R,S), their
+    pre-quantisation values in code units, the P scale of each (row, block),
+    the BLASST predicate margins (B,H,R,blocks), the per-row skipped-block
+    counts and ``flip_allowance`` (B,H,R,D): the largest output change that
+    one-step flips of P codes lying within 2^-15 (relative) of an E4M3
+    rounding midpoint could cause -- the codes that fp32-level differences in
+    evaluating the same scores (exp2, reciprocals, summation order) can flip."""
     B, H, S, D = q.shape
     dev_rows = torch.arange(S) if rows is None else torch.as_tensor(rows)
     R = dev_rows.numel()
@@ -152,7 +180,15 @@ def attention(q, k, v, v_scale, *, sm_scale, p_max_offset, block_m=64, block_n=6
     skipped = torch.zeros(B, H, R)
     total = torch.zeros(B, H, R)
     row_valid = (dev_rows < S).float()
-    dbg = {"skip": []} if return_debug else None
+    dbg = {"skip": [], "codes": [], "x": [], "sP": [], "s": [], "margin": []} if return_debug else None
+    if dbg is not None:
+        # output change that one-step flips of rounding-edge P codes could cause
+        alw = torch.zeros(B, H, R, D)
+        alw_c = torch.zeros(B, H, R, D)
+    if scores_log2 is not None:
+        scores_log2 = scores_log2.float()
+        if scores_log2.shape != (B, H, R, S):
+            raise ValueError(f"scores_log2 must be {(B, H, R, S)}; got {tuple(scores_log2.shape)}")
 
     for start_n in range(0, S, block_n):
         n1 = min(start_n + block_n, S)
@@ -163,12 +199,16 @@ def attention(q, k, v, v_scale, *, sm_scale, p_max_offset, block_m=64, block_n=6
         kb[:, :, :nb] = kf[:, :, start_n:n1]
         vb = torch.zeros(B, H, block_n, D)
         vb[:, :, :nb] = vf[:, :, start_n:n1]
-        s = torch.matmul(qf, kb.transpose(-2, -1)) * sm
-        if has_qm:
-            ksb = torch.zeros(B, H, block_n, D)
-            ksb[:, :, :nb] = ks[:, :, start_n:n1]
-            corr = torch.matmul(qm_rows, ksb.transpose(-2, -1)) * sm
-            s = s + corr
+        if scores_log2 is None:
+            s = torch.matmul(qf, kb.transpose(-2, -1)) * sm
+            if has_qm:
+                ksb = torch.zeros(B, H, block_n, D)
+                ksb[:, :, :nb] = ks[:, :, start_n:n1]
+                corr = torch.matmul(qm_rows, ksb.transpose(-2, -1)) * sm
+                s = s + corr
+        else:
+            s = torch.zeros(B, H, R, block_n)
+            s[..., :nb] = scores_log2[..., start_n:n1] / _f32(LOG2E)
         s = torch.where(col_mask, s, torch.tensor(-math.inf))
 
         skip = torch.zeros(B, H, R, dtype=torch.bool)
@@ -181,6 +221,9 @@ def attention(q, k, v, v_scale, *, sm_scale, p_max_offset, block_m=64, block_n=6
             m_ij = torch.where(skip, m_i, m_ij)
             skipped += skip.float()
             total += row_valid
+            if dbg is not None:
+                # distance of the skip predicate from its threshold (skip iff < 0)
+                dbg["margin"].append((block_max - torch.maximum(m_i, block_max)) - log_lam)
         elif rowmax_est is not None:
             if p_kind == 2:
                 block_max = s.amax(-1)
@@ -269,19 +312,48 @@ def attention(q, k, v, v_scale, *, sm_scale, p_max_offset, block_m=64, block_n=6
 
         l_i = l_i * alpha + p.sum(-1)
 
+        # x: P in code units; codes = e4m3(x) (saturating); p_deq = bf16(code * s_P)
         if p_kind == 0:
-            p_deq = _e4m3_sat(p).to(torch.bfloat16).float()
+            sP = torch.ones(B, H, R)
+            x = p
         elif p_kind == 1:
             ra = p.abs().amax(-1).clamp_min(float(np.float32(1e-4)))
             e = np.clip(ceil_log2_exact((ra / _f32(FP8_MAX)).numpy()), -127, 127)
             sP = torch.from_numpy(np.ldexp(np.float32(1.0), e).astype(np.float32))
-            ps = torch.clamp(p / sP[..., None], -FP8_MAX, FP8_MAX)
-            p_deq = (_e4m3_sat(ps) * sP[..., None]).to(torch.bfloat16).float()
+            x = torch.clamp(p / sP[..., None], -FP8_MAX, FP8_MAX)
         else:
             ra = p.abs().amax(-1).clamp_min(float(np.float32(1e-12)))
             sP = ra / _f32(FP8_MAX)
-            ps = torch.clamp(p / sP[..., None], -FP8_MAX, FP8_MAX)
-            p_deq = (_e4m3_sat(ps) * sP[..., None]).to(torch.bfloat16).float()
+            x = torch.clamp(p / sP[..., None], -FP8_MAX, FP8_MAX)
+        codes = torch.from_numpy(fp8.encode(x.contiguous().numpy()))
+        if force_codes is not None:
+            fc, fm = force_codes
+            codes[..., :nb] = torch.where(fm[..., start_n:n1], fc[..., start_n:n1], codes[..., :nb])
+        vals = torch.from_numpy(fp8.decode(codes.numpy()))
+        if p_kind == 0:
+            p_deq = vals.to(torch.bfloat16).float()
+        else:
+            p_deq = (vals * sP[..., None]).to(torch.bfloat16).float()
+        if dbg is not None:
+            edge = rounding_edge_step(x)
+            if p_kind == 1:
+                # an MX exponent at a power-of-two edge re-rounds every code of the block
+                lr = np.log2((ra / _f32(FP8_MAX)).double().numpy())
+                e_edge = torch.from_numpy(np.abs(lr - np.round(lr)) <= EDGE_REL)
+                step_all = 2.0 * rounding_edge_step(x, rel=1.0)
+                edge = torch.where(e_edge[..., None], step_all, edge)
+            w = torch.where(col_mask, edge * sP[..., None], torch.zeros_like(edge))
+            dpv = torch.matmul(w, vb.abs())
+            if v_block_scale is not None:
+                dpv = dpv * v_block_scale.float()[:, start_n // v_block_size, :].abs()[..., None, None]
+            alw = alw * alpha[..., None] + dpv
+            if v_alpha is not None:
+                alw_c = alw_c * alpha[..., None] + w.sum(-1)[..., None] * v_alpha.float()[
+                    :, start_n // v_smooth_block].abs()[:, :, None, :]
+            dbg["s"].append(s[..., :nb].clone())
+            dbg["codes"].append(codes[..., :nb].clone())
+            dbg["x"].append(x[..., :nb].clone())
+            dbg["sP"].append(sP.clone())
 
         pv = torch.matmul(p_deq, vb)
         if v_block_scale is not None:
@@ -311,5 +383,13 @@ def attention(q, k, v, v_scale, *, sm_scale, p_max_offset, block_m=64, block_n=6
             st[bi, :, 1] = tt[:, sel].sum(-1)
         result.append(st)
     if dbg is not None:
+        dbg["codes"] = torch.cat(dbg["codes"], -1)
+        dbg["x"] = torch.cat(dbg["x"], -1)
+        dbg["sP"] = torch.stack(dbg["sP"], -1)
+        dbg["s"] = torch.cat(dbg["s"], -1)
+        dbg["margin"] = torch.stack(dbg["margin"], -1) if dbg["margin"] else None
+        dbg["row_skips"] = skipped
+        scale_main = 1.0 if v_block_scale is not None else v_scale.float().abs()[:, :, None, :]
+        dbg["flip_allowance"] = (alw * scale_main + alw_c) / l_i[..., None].abs()
         result.append(dbg)
     return result[0] if len(result) == 1 else tuple(result)

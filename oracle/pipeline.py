@@ -110,10 +110,16 @@ def qk_quant_inputs(q_work, k_work, cfg):
 
 
 def p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype, rows=None,
-                   return_blasst_stats=False, qk_dequant_dtype=torch.bfloat16):
+                   return_blasst_stats=False, qk_dequant_dtype=torch.bfloat16, scores_log2=None,
+                   return_debug=False, force_codes=None, rowmax_log2=None):
     """``qk_dequant_dtype=torch.bfloat16`` is the reference (attention.py:534-535);
     ``torch.float32`` keeps the dequantised Q/K exact and is used only to measure
-    how sensitive the reference output is to that rounding."""
+    how sensitive the reference output is to that rounding.  ``scores_log2``,
+    ``return_debug`` and ``force_codes`` are passed to ``attention.attention``
+    (rows in the reordered order of the work tensors); ``rowmax_log2``
+    (B,H,G), when given, replaces the qm_k row-max estimate (log2 units, one
+    value per Q group) -- used with ``scores_log2`` to replay the reference
+    algorithm on another implementation's scores and estimate."""
     b, s, h, d = q_work.shape
     qi, ki = qk_quant_inputs(q_work, k_work, cfg)
     qc, qs, qmeta = quant_qk(qi, cfg)
@@ -141,8 +147,12 @@ def p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype
     if cfg.rowmax_mode == "qm_k":
         if qm is None:
             raise ValueError("rowmax_mode='qm_k' requires smoothing='full' so qm exists")
-        rowmax_est = oattn.estimate_rowmax_qm_k(qm, k_work, block_q=cfg.q_smooth_block_size,
-                                                sm_scale=sm_scale)
+        if rowmax_log2 is None:
+            rowmax_est = oattn.estimate_rowmax_qm_k(qm, k_work, block_q=cfg.q_smooth_block_size,
+                                                    sm_scale=sm_scale)
+        else:
+            rowmax_est = (rowmax_log2.float() / torch.tensor(oattn.LOG2E, dtype=torch.float32)).repeat_interleave(
+                cfg.q_smooth_block_size, dim=2).contiguous()
     elif cfg.rowmax_mode != "online":
         raise ValueError(f"unsupported rowmax_mode: {cfg.rowmax_mode!r}")
     p_mode = cfg.p_quant
@@ -158,11 +168,11 @@ def p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype
         v_block_scale=v_block_scale, v_block_size=v_block_size, p_quant_mode=p_mode,
         rowmax_est=rowmax_est, blasst_lambda=cfg.blasst_lambda, blasst_fill_mode=cfg.blasst_fill,
         blasst_fill_alpha=cfg.blasst_fill_alpha, blasst_uta_bins=cfg.blasst_uta_bins,
-        return_blasst_stats=return_blasst_stats, rows=rows)
-    if return_blasst_stats:
-        o, st = res
-        return o.permute(*perm).contiguous().to(out_dtype), st
-    return res.permute(*perm).contiguous().to(out_dtype)
+        return_blasst_stats=return_blasst_stats, rows=rows, return_debug=return_debug,
+        scores_log2=scores_log2, force_codes=force_codes)
+    res = list(res) if isinstance(res, tuple) else [res]
+    res[0] = res[0].permute(*perm).contiguous().to(out_dtype)
+    return res[0] if len(res) == 1 else tuple(res)
 
 
 def sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype):
@@ -195,7 +205,11 @@ def sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype):
 
 
 def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=False,
-                         qk_dequant_dtype=torch.bfloat16):
+                         qk_dequant_dtype=torch.bfloat16, scores_log2=None, return_debug=False,
+                         force_codes=None, rowmax_log2=None):
+    """Output in the caller's row order.  With ``return_debug`` the debug dict of
+    ``attention.attention`` (reordered row order) follows, plus ``"order"``
+    (the Q k-means order, or None)."""
     if q.shape != k.shape or q.shape != v.shape:
         raise ValueError("q/k/v shapes must match")
     out_dtype = q.dtype
@@ -206,15 +220,32 @@ def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=Fal
     if cfg.blasst_lambda is not None and not cfg.p_requant:
         raise ValueError("BLASST skip/fill requires cfg.p_requant=True")
     q_work, k_work, v_work, qm, v_alpha, q_km, _ = preprocess(q, k, v, cfg)
-    stats = None
+    stats = dbg = None
     if cfg.p_requant:
         r = p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype,
-                           return_blasst_stats=return_blasst_stats, qk_dequant_dtype=qk_dequant_dtype)
-        o, stats = r if return_blasst_stats else (r, None)
+                           return_blasst_stats=return_blasst_stats, qk_dequant_dtype=qk_dequant_dtype,
+                           scores_log2=scores_log2, return_debug=return_debug, force_codes=force_codes,
+                           rowmax_log2=rowmax_log2)
+        r = list(r) if isinstance(r, tuple) else [r]
+        o = r.pop(0)
+        stats = r.pop(0) if return_blasst_stats else None
+        dbg = r.pop(0) if return_debug else None
+        if dbg is not None:
+            dbg["order"] = q_km["order"] if q_km is not None else None
     else:
         o = sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype).to(out_dtype)
+    if dbg is not None:
+        dbg["flip_allowance_nhd"] = dbg["flip_allowance"].permute(0, 2, 1, 3).contiguous()
     if q_km is not None:
         inv = q_km["inverse_order"]
-        ob = o.permute(0, 2, 1, 3).reshape(b * h, s, d)
-        o = torch.gather(ob, 1, inv.unsqueeze(-1).expand(-1, -1, d)).reshape(b, h, s, d).permute(0, 2, 1, 3).contiguous()
-    return (o, stats) if return_blasst_stats else o
+
+        def unreorder(t):
+            tb = t.permute(0, 2, 1, 3).reshape(b * h, s, d)
+            return torch.gather(tb, 1, inv.unsqueeze(-1).expand(-1, -1, d)).reshape(b, h, s, d).permute(
+                0, 2, 1, 3).contiguous()
+
+        o = unreorder(o)
+        if dbg is not None:
+            dbg["flip_allowance_nhd"] = unreorder(dbg["flip_allowance_nhd"])
+    out = [o] + ([stats] if return_blasst_stats else []) + ([dbg] if return_debug else [])
+    return out[0] if len(out) == 1 else tuple(out)

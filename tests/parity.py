@@ -1,0 +1,245 @@
+"""Parity helpers shared by the GPU attention tests and the smoke check.
+
+The attention kernel is checked in three parts, each against the CPU oracle
+(the restatement of the reference path, ``oracle/``):
+
+1. **Scores.**  ``lbfq_attention_scores`` returns the kernel's log2-unit
+   scores, formed with the kernel's own MFMA sequence.  They must equal the
+   exact scores of the same FP8 codes (float64 products and sums) within the
+   accumulation error of the gfx950 FP8 MFMA: measured at <= 3.4e-4 *
+   max|a| * max|b| per 32x32x64 MFMA, bounded here by ``MFMA_REL = 2^-10``
+   (plus fp32 rounding of the scale products).
+2. **Everything after the scores.**  The oracle replays the reference
+   algorithm (row max, thresholds, BLASST, P quantisation, PV, V scales,
+   smoothing, epilogue; ``attention_triton.py:163-407``) on the kernel's
+   scores and row-max estimate.  The kernel's output must match that replay
+   within the north-star tolerance: cosine >= 0.9999 and |diff| <= 1e-2 --
+   or one bf16 ulp of the value where that is larger (both sides round an
+   fp32 result to bf16; at |o| >= 2 one ulp is 1/64).  BLASST skip decisions
+   and statistics must match the replay exactly.
+3. **Against the reference itself** (the oracle with its own bf16-dequant
+   scores, ``attention.py:532-535``): cosine >= 0.9999 for the dense
+   configurations.  Element-wise agreement to 1e-2 is not attainable by an
+   FP8-MFMA kernel: the reference rounds the dequantised Q/K to bf16 (up to
+   2^-9 relative per operand) and the MFMA accumulates with ~2^-12 relative
+   error; both perturb the scores, which flips E4M3 P codes at rounding
+   boundaries and moves the P scales and row sums.  Item 2 shows that every
+   difference comes from the scores; the tests record the reference gap.
+   BLASST decisions must agree with the reference except in rows whose
+   predicate margin is within the score perturbation of ln(lambda).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from oracle import fp8
+from oracle import pipeline as opipe
+
+COS_MIN = 0.9999
+MAXABS = 1e-2
+MFMA_REL = 2.0 ** -10
+LOG2E = 1.4426950408889634
+
+
+def cosine(a, b) -> float:
+    a, b = a.float().flatten(), b.float().flatten()
+    return torch.nn.functional.cosine_similarity(a.unsqueeze(0), b.unsqueeze(0)).item()
+
+
+def ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    a = x.float().abs().clamp_min(2.0 ** -126)
+    return torch.pow(2.0, torch.floor(torch.log2(a)) - 7)
+
+
+def tolerance(ref: torch.Tensor) -> torch.Tensor:
+    """max(1e-2, one bf16 ulp of the reference value), element-wise."""
+    return torch.maximum(torch.full(ref.shape, MAXABS), ulp_bf16(ref))
+
+
+def kernel_operands(q, k, v, cfg, dev, sm_scale=None):
+    """The quantised operands exactly as fake_quant_attention builds them."""
+    from low_bit_fake_quant.attention import _lazy_preprocess, quantize_operands
+    sm = q.shape[-1] ** -0.5 if sm_scale is None else sm_scale
+    prep = _lazy_preprocess(q.to(dev), k.to(dev), v.to(dev), cfg)
+    return quantize_operands(prep, cfg, sm), sm
+
+
+def kernel_scores(ops, cfg, sm, rows=None) -> torch.Tensor:
+    """(B, H, R, S) log2-unit scores of the kernel (rows in its reordered order), CPU."""
+    from low_bit_fake_quant.attention_kernel import attention_scores
+    u = attention_scores(ops, cfg, sm, rows=rows)
+    return u.reshape(ops.b, ops.h, -1, ops.s).cpu()
+
+
+def replay(q, k, v, cfg, ops, u, **kw):
+    """The oracle's reference algorithm on the kernel's scores and row-max
+    estimate; returns (output, ..., debug) with the debug dict last."""
+    rm = ops.rowmax.cpu() if ops.rowmax is not None else None
+    return opipe.fake_quant_attention(q, k, v, cfg, scores_log2=u, rowmax_log2=rm, return_debug=True, **kw)
+
+
+def check_against_replay(out, q, k, v, cfg, ops, u, label=""):
+    """Replay + strict check; returns (cos, max|diff|, replay output, replay debug)."""
+    rep, dbg = replay(q, k, v, cfg, ops, u)
+    c, m = strict_check(out, rep, label, allowance=dbg["flip_allowance_nhd"])
+    return c, m, rep, dbg
+
+
+def strict_check(out, rep, label="", allowance=None):
+    """North-star tolerance against the replay; returns (cos, max|diff|).
+    ``allowance`` (the replay's ``flip_allowance``, same layout as the
+    output) adds, per element, the change that one-step flips of P codes
+    within 2^-15 of an E4M3 rounding midpoint could cause: codes that the two
+    sides' fp32-level differences in evaluating the same scores (hardware
+    exp2 and reciprocal vs torch) can round either way.  Elements that need
+    it are counted in the message."""
+    out, rep = out.float().cpu(), rep.float().cpu()
+    fin = torch.isfinite(rep)
+    assert torch.equal(torch.isfinite(out), fin), f"{label}: non-finite outputs differ from the replay"
+    d = (out - rep).abs()[fin]
+    tol = tolerance(rep[fin])
+    over = d > tol
+    if allowance is not None:
+        tol = tol + allowance.float().cpu()[fin]
+    bad = d > tol
+    c = cosine(out[fin], rep[fin])
+    assert c >= COS_MIN and not bad.any(), (
+        f"{label}: vs replay cos={c:.7f} max|diff|={d.max():.3e} elements beyond tolerance={int(bad.sum())} "
+        f"(beyond 1e-2 / 1 ulp before the flip allowance: {int(over.sum())})")
+    if over.any():
+        print(f"{label}: {int(over.sum())} elements within the rounding-edge flip allowance")
+    return c, d.max().item()
+
+
+def exact_scores_and_bound(ops, cfg, sm):
+    """float64 scores of the kernel's FP8 codes (exact products and sums) and a
+    bound on the kernel's error: the MFMA accumulation (MFMA_REL of max|a|max|b|
+    and of the accumulator input, per 64-wide MFMA) plus fp32 roundings of the
+    scale products and of the qm correction's start value.  (B,H,S,S) each."""
+    S, D = ops.s, ops.d
+    qc = torch.from_numpy(fp8.decode(ops.q_codes.cpu().numpy())).double()[:, :, :S]
+    kc = torch.from_numpy(fp8.decode(ops.k_codes.cpu().numpy())).double()[:, :, :S]
+    sml2 = float(np.float32(np.float32(sm) * np.float32(LOG2E)))
+    if cfg.qk_quant == "mxfp8":
+        qe = torch.from_numpy(ops.q_scale.cpu().numpy().astype(np.int64))[:, :, :S]
+        ke = torch.from_numpy(ops.k_scale.cpu().numpy().astype(np.int64))[:, :, :S]
+        qv = qc * torch.pow(2.0, (qe - 127).double()).repeat_interleave(32, -1)
+        kv = kc * torch.pow(2.0, (ke - 127).double()).repeat_interleave(32, -1)
+        C = torch.full((1, 1, S, S), sml2, dtype=torch.float64)
+    else:
+        blk = cfg.fp8_block_size
+        qs = ops.q_scale.cpu().double().repeat_interleave(blk, -1)[:, :, :S]
+        ks = ops.k_scale.cpu().double().repeat_interleave(blk, -1)[:, :, :S]
+        qv, kv = qc, kc
+        C = sml2 * qs[..., :, None] * ks[..., None, :]
+    dot = torch.zeros(qv.shape[0], qv.shape[1], S, S, dtype=torch.float64)
+    bias = torch.zeros_like(dot)
+    if ops.bias is not None:
+        g = cfg.q_smooth_block_size
+        b = ops.bias.cpu().double()[..., :S]                      # (B,H,G,S)
+        bias = b.repeat_interleave(g, 2)[:, :, :S]
+    err = torch.zeros_like(dot)
+    acc_in = bias / C
+    for hh in range(D // 64):
+        qh, kh = qv[..., 64 * hh:64 * hh + 64], kv[..., 64 * hh:64 * hh + 64]
+        part = torch.matmul(qh, kh.transpose(-2, -1))
+        mq, mk = qh.abs().amax(-1), kh.abs().amax(-1)
+        err += MFMA_REL * (mq[..., :, None] * mk[..., None, :] + acc_in.abs())
+        dot += part
+        acc_in = bias / C + dot
+    u = dot * C + bias
+    bound = err * C + 2.0 ** -20 * (u.abs() + bias.abs()) + 1e-30
+    return u, bound
+
+
+def flipped_codes(dbg_a, dbg_b):
+    """Positions whose E4M3 P codes differ between two oracle runs, and whether
+    every such pair of codes is one E4M3 step apart with the pre-quantisation
+    values on either side of the rounding midpoint between them."""
+    ca, cb = dbg_a["codes"], dbg_b["codes"]
+    diff = ca != cb
+    if not diff.any():
+        return diff, True
+    va = torch.from_numpy(fp8.decode(ca[diff].numpy())).double()
+    vb = torch.from_numpy(fp8.decode(cb[diff].numpy())).double()
+    xa, xb = dbg_a["x"][diff].double(), dbg_b["x"][diff].double()
+    lo, hi = torch.minimum(va, vb), torch.maximum(va, vb)
+    # adjacent magnitudes: no E4M3 value strictly between them
+    allv = torch.from_numpy(np.unique(np.abs(fp8.DECODE[~np.isnan(fp8.DECODE)]))).double()
+    idx_lo = torch.searchsorted(allv, lo.abs().contiguous())
+    idx_hi = torch.searchsorted(allv, hi.abs().contiguous())
+    same_sign = (torch.sign(va) == torch.sign(vb)) | (va == 0) | (vb == 0)
+    adjacent = ((idx_hi - idx_lo).abs() == 1) & same_sign
+    mid = (lo + hi) / 2
+    straddle = ((xa - mid) * (xb - mid) <= 0)
+    return diff, bool((adjacent & straddle).all())
+
+
+def skip_agreement(rsk_kernel, dbg_ref, u_kernel, order):
+    """Per-row skip counts of the kernel vs the reference (oracle with its own
+    scores).  Rows where any block's predicate margin is within twice the
+    largest score difference of that row (natural units) are excluded.
+    Returns (rows compared, rows excluded, disagreeing compared rows)."""
+    s_ref = dbg_ref["s"].double()                       # natural units, reordered rows
+    s_ker = u_kernel.double() / LOG2E
+    fin = torch.isfinite(s_ref) & torch.isfinite(s_ker)
+    gap = torch.where(fin, (s_ref - s_ker).abs(), torch.zeros_like(s_ref)).amax(-1)   # (B,H,R)
+    margin = dbg_ref["margin"].double()                 # (B,H,R,blocks)
+    near = (margin.abs() < 2 * gap[..., None] + 1e-6).any(-1)
+    rs_ref = dbg_ref["row_skips"]
+    b, h, r = rs_ref.shape
+    rs_ref = rs_ref.reshape(b * h, r)
+    near = near.reshape(b * h, r)
+    if order is not None:
+        rs_o, near_o = torch.empty_like(rs_ref), torch.empty_like(near)
+        rs_o.scatter_(1, order.long(), rs_ref)
+        near_o.scatter_(1, order.long(), near)
+        rs_ref, near = rs_o, near_o
+    rsk = rsk_kernel.cpu()
+    cmp = ~near
+    return int(cmp.sum()), int(near.sum()), int((rsk[cmp] != rs_ref[cmp]).sum())
+
+
+def sampled_rows(q, k, v, cfg, ops, rows, sm):
+    """Replay and reference for a sample of rows of the kernel's reordered row
+    order (full-length checks; every head has its own k-means order).
+    Returns (caller rows (B*H, R), scores, replay (B,R,H,D), reference
+    (B,R,H,D), replay debug); the oracle's preprocess runs once."""
+    qw, kw, vw, qm, v_alpha, q_km, _ = opipe.preprocess(q, k, v, cfg)
+    rows = rows.sort().values
+    if q_km is not None:
+        caller = q_km["order"][:, rows]
+    else:
+        caller = rows.unsqueeze(0).expand(ops.b * ops.h, -1)
+    u = kernel_scores(ops, cfg, sm, rows=rows.to(torch.int32))
+    rm = ops.rowmax.cpu() if ops.rowmax is not None else None
+    rep, dbg_rep = opipe.p_requant_path(qw, kw, vw, qm, v_alpha, cfg, sm, torch.float32, rows=rows,
+                                        scores_log2=u, rowmax_log2=rm, return_debug=True)
+    ref = opipe.p_requant_path(qw, kw, vw, qm, v_alpha, cfg, sm, torch.float32, rows=rows)
+    return caller, u, rep, ref, dbg_rep
+
+
+def gather_caller_rows(out: torch.Tensor, caller: torch.Tensor) -> torch.Tensor:
+    """out (B,S,H,D) in caller order -> (B,R,H,D) at each head's caller rows."""
+    b, s, h, d = out.shape
+    idx = caller.reshape(b, h, -1).permute(0, 2, 1)                       # (B,R,H)
+    return torch.gather(out, 1, idx.unsqueeze(-1).expand(-1, -1, -1, d))
+
+
+def unpermute_rows(t: torch.Tensor, order) -> torch.Tensor:
+    """(B*H, S) in reordered row order -> caller row order."""
+    if order is None:
+        return t
+    o = torch.empty_like(t)
+    o.scatter_(1, order.long(), t)
+    return o
+
+
+__all__ = ["COS_MIN", "MAXABS", "MFMA_REL", "cosine", "ulp_bf16", "tolerance", "kernel_operands", "kernel_scores",
+           "replay", "strict_check", "check_against_replay", "exact_scores_and_bound", "flipped_codes",
+           "skip_agreement", "sampled_rows", "gather_caller_rows", "unpermute_rows",
+           "math"]

@@ -263,3 +263,84 @@ def test_parse_blasst_fill_spellings():
     assert P("uta16_a1.5", alpha=1.0, uta_bins=8) == (oattn.FILL_UTA, 1.5, 16)
     with pytest.raises(ValueError, match="unknown blasst_fill_mode"):
         P("median", alpha=1.0, uta_bins=16)
+
+
+# ---- replay on supplied scores, forced P codes, rounding-edge allowance ------------
+
+
+@pytest.mark.parametrize("p_mode", ["elementwise", "mx", "dynamic"])
+def test_supplied_log2_scores_replace_the_score_computation(p_mode):
+    """scores_log2 stands in for q.k * sm_scale (+ correction): integer log2
+    scores plus an arbitrary integer per-(row, key) term reproduce the dense
+    float64 softmax, whatever q and k hold."""
+    q, k, v, vs = _exact_case(s=200, seed=21, lo=-5, hi=5)
+    g = torch.Generator().manual_seed(5)
+    # scores stay within [-6, 6], so every P (>= 2^(8-12)) is a normal E4M3 value
+    extra = torch.randint(-1, 2, (1, 2, 200, 200), generator=g).double()
+    u = torch.matmul(q.double(), k.double().transpose(-2, -1)) + extra
+    junk_q, junk_k = torch.randn(q.shape, generator=g).bfloat16(), torch.randn(k.shape, generator=g).bfloat16()
+    out = oattn.attention(junk_q, junk_k, v, vs, sm_scale=0.37, p_max_offset=8, p_quant_mode=p_mode,
+                          scores_log2=u.float())
+    ref = _dense(q, k, v.double() * vs.double()[:, :, None, :], extra=extra)
+    _assert_close_bf16(out, ref)
+
+
+def test_forced_codes_change_the_output_by_their_value_change():
+    """force_codes replaces P codes before dequantisation: with exact
+    (power-of-two) P, moving the codes of one key in every row by one E4M3
+    step changes each output row by (new - old) * v_key / l exactly (l, the
+    pre-quantisation row sum, is unchanged)."""
+    q, k, v, vs = _exact_case(s=128, seed=22)
+    kw = dict(sm_scale=LN2, p_max_offset=8, p_quant_mode="elementwise")
+    out, dbg = oattn.attention(q, k, v, vs, return_debug=True, **kw)
+    codes = dbg["codes"].clone()
+    mask = torch.zeros_like(codes, dtype=torch.bool)
+    j = 37
+    mask[..., j] = True
+    new = codes.clone()
+    new[..., j] = torch.where(codes[..., j] == 0, codes[..., j], codes[..., j] + 1)  # one step up (finite codes)
+    out2 = oattn.attention(q, k, v, vs, force_codes=(new, mask), **kw)
+    old_v = torch.from_numpy(fp8.decode(codes[..., j].numpy())).double()
+    new_v = torch.from_numpy(fp8.decode(new[..., j].numpy())).double()
+    l = dbg["x"].double().sum(-1)          # elementwise: p in code units is p itself
+    vj = (v.double() * vs.double()[:, :, None, :])[:, :, j, :]                     # (B,H,D)
+    expect = out.double() + ((new_v - old_v) / l)[..., None] * vj[:, :, None, :]
+    _assert_close_bf16(out2, expect, ulps=1.0)
+
+
+def test_rounding_edge_step():
+    """The E4M3 step at a rounding midpoint within 2^-15 of |x|, else 0."""
+    mid = 1.0625                                              # between 1.0 and 1.125
+    x = torch.tensor([mid * (1 + 2.0 ** -17), mid * (1 - 2.0 ** -17), mid * (1 + 2.0 ** -12), 1.0, 448.0,
+                      2.0 ** -10, -mid * (1 + 2.0 ** -18), 240.0, 232.0 * (1 + 2.0 ** -20)], dtype=torch.float32)
+    got = oattn.rounding_edge_step(x)
+    want = torch.tensor([0.125, 0.125, 0.0, 0.0, 0.0, 2.0 ** -9, 0.125, 0.0, 16.0])
+    assert torch.equal(got, want)
+
+
+def test_flip_allowance_bounds_flips_of_edge_codes():
+    """Scores placed so that many P values sit on E4M3 rounding midpoints
+    (u = log2(1.0625) + integer): flipping every such code to its other
+    neighbour moves each output by no more than the reported allowance, and
+    the allowance is zero where no code is at an edge."""
+    q, k, v, vs = _exact_case(s=128, seed=23)
+    u = torch.matmul(q.double(), k.double().transpose(-2, -1))
+    g = torch.Generator().manual_seed(7)
+    edge = torch.rand(u.shape, generator=g) < 0.3
+    u = (u + torch.where(edge, torch.tensor(math.log2(1.0625)), torch.tensor(0.0))).float()
+    kw = dict(sm_scale=LN2, p_max_offset=8, p_quant_mode="elementwise", scores_log2=u)
+    out, dbg = oattn.attention(q, k, v, vs, return_debug=True, **kw)
+    step = oattn.rounding_edge_step(dbg["x"])
+    assert (step > 0).float().mean() > 0.02   # (rows whose max sits on an edge shift off it)
+    vals = torch.from_numpy(fp8.decode(dbg["codes"].numpy())).double()
+    x = dbg["x"].double()
+    # the other neighbour of each edge value
+    other = torch.where(vals >= x, vals - step.double(), vals + step.double()).float()
+    flip = torch.from_numpy(fp8.encode(other.numpy()))
+    out2 = oattn.attention(q, k, v, vs, force_codes=(flip, step > 0), **kw)
+    alw = dbg["flip_allowance"]
+    err = (out2.double() - out.double()).abs()
+    assert (err <= alw.double() + 2 * _bf16_ulp(out.float()).double()).all()
+    out0, dbg0 = oattn.attention(q, k, v, vs, return_debug=True, sm_scale=LN2, p_max_offset=8,
+                                 p_quant_mode="elementwise")
+    assert dbg0["flip_allowance"].abs().max() == 0.0
