@@ -11,7 +11,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._ops import qmk
+from ._ops import RowSource, qmk
 from .config import QuantConfig
 from .hadamard import apply_qk_hadamard
 from .kmeans import KMeansReorderResult, q_kmeans_reorder
@@ -57,7 +57,7 @@ def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cfg: QuantCon
     elif cfg.smoothing == "full":
         k_work, k_mean = smooth_k(k_work)
         q_work, qm = group_mean_q(q_work, block_q=cfg.q_smooth_block_size)
-        bias, _ = qmk(qm, k_work, 1.0, s_pitch=k_work.shape[1], want_rowmax=False)   # (B,H,G,S)
+        bias, _ = qmk(qm, RowSource(k_work), 1.0, s_pitch=k_work.shape[1], want_rowmax=False)   # (B,H,G,S)
         correction = bias.permute(0, 2, 1, 3).contiguous().to(cfg.correction_dtype)  # (B,G,H,S)
     elif cfg.smoothing != "off":
         raise ValueError(f"unsupported smoothing mode: {cfg.smoothing!r}")

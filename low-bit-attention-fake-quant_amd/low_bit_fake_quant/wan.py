@@ -79,9 +79,11 @@ def workloads() -> dict:
                      v_mxfp8_block_size=64, v_kmeans_k=64, v_smooth_mode="per_block", v_smooth_block_size=64,
                      smoothing="full", q_kmeans_k=32, p_requant=True, p_quant="mx", rowmax_mode="online",
                      p_requant_block_m=64, p_requant_block_n=64)
+    # lambda frozen once by calibrate_blasst_lambda on the full 40-head x 75600
+    # workload (seed 0): 50.0% of the (row, K-block) decisions skip
     c4 = QuantConfig(qk_quant="fp8_block", fp8_block_size=64, v_quant="fp8_channel", smoothing="full",
                      q_smooth_block_size=256, q_kmeans_k=32, p_requant=True, p_quant="dynamic",
-                     rowmax_mode="qm_k", p_requant_block_m=64, p_requant_block_n=64, blasst_lambda=0.02,
+                     rowmax_mode="qm_k", p_requant_block_m=64, p_requant_block_n=64, blasst_lambda=1.59e-9,
                      blasst_fill="mean_a1.5")
     return {
         0: Workload("plumbing_h2_n1024_d64", 2, 1024, 64, c0),
@@ -137,3 +139,60 @@ def make_inputs(w: Workload, *, seed: int = 0, heads: int | None = None, dtype=t
         q = q + f
         k = k + f
     return tuple(t.unsqueeze(0).to(dtype).contiguous() for t in (q, k, v))
+
+
+def blasst_skip_rate(q, k, v, cfg, lam: float) -> float:
+    """Fraction of (row, K-block) decisions BLASST skips at lambda ``lam``:
+    stats[..., 0].sum() / stats[..., 1].sum() (attention_triton.py:404-407),
+    for (B,S,H,D) device tensors already padded to the block LCM."""
+    import dataclasses
+
+    from .attention import _lazy_preprocess, quantize_operands
+    from .attention_kernel import launch_attention
+    sm = q.shape[-1] ** -0.5
+    c = dataclasses.replace(cfg, blasst_lambda=float(lam))
+    ops = quantize_operands(_lazy_preprocess(q, k, v, c), c, sm)
+    _, stats = launch_attention(ops, c, sm, q.dtype, return_blasst_stats=True)
+    st = stats.sum(dim=(0, 1))
+    return (st[0] / st[1]).item()
+
+
+def calibrate_blasst_lambda(q, k, v, cfg, target: float = 0.5, iters: int = 24) -> tuple[float, float]:
+    """Bisection on log(lambda) for the skip rate ``target`` (the skip rate
+    grows with lambda).  Returns (lambda, measured skip rate)."""
+    lo, hi = math.log(1e-12), math.log(0.999)
+    best = (math.exp(hi), blasst_skip_rate(q, k, v, cfg, math.exp(hi)))
+    for _ in range(iters):
+        mid = 0.5 * (lo + hi)
+        r = blasst_skip_rate(q, k, v, cfg, math.exp(mid))
+        if abs(r - target) < abs(best[1] - target):
+            best = (math.exp(mid), r)
+        if r > target:
+            hi = mid
+        else:
+            lo = mid
+    return best
+
+
+def _main(argv=None) -> int:
+    import argparse
+    import json
+    import sys
+    ap = argparse.ArgumentParser(description="Calibrate BLASST lambda of a Wan workload on the GPU")
+    ap.add_argument("--config", type=int, default=4)
+    ap.add_argument("--target", type=float, default=0.5)
+    ap.add_argument("--heads", type=int, default=0)
+    args = ap.parse_args(argv)
+    w = workloads()[args.config]
+    q, k, v = make_inputs(w, seed=0, heads=args.heads or None)
+    q, k, v, _ = pad_qkv(q, k, v, w.cfg)
+    dev = torch.device("cuda:0")
+    lam, rate = calibrate_blasst_lambda(q.to(dev), k.to(dev), v.to(dev), w.cfg, target=args.target)
+    print(json.dumps({"config": args.config, "workload": w.name, "heads": q.shape[2], "lambda": lam,
+                      "skip_rate": rate, "target": args.target}))
+    sys.stdout.flush()
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(_main())

@@ -9,7 +9,10 @@ Follows ``attention.py`` of the reference:
 * ``p_requant_path``       -- ``attention.py:505-639`` (V kind marshalling,
                               rowmax estimate, P mode, kernel call);
 * ``sdpa_path``            -- ``attention.py:247-321``;
-* ``fake_quant_attention`` -- ``attention.py:706-806`` (guards, inverse Q gather).
+* ``fake_quant_attention`` -- ``attention.py:706-806`` (guards, inverse Q gather);
+* ``prepare_qkv``          -- the legacy pipeline ``pipeline.py:42-110`` (Q k-means,
+                              smoothing with the qm.K_s correction, Hadamard on the
+                              smoothed tensors, then quantisation).
 
 ``cfg`` is any object with the ``QuantConfig`` fields.  All tensors are CPU.
 
@@ -249,3 +252,32 @@ def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=Fal
             dbg["flip_allowance_nhd"] = unreorder(dbg["flip_allowance_nhd"])
     out = [o] + ([stats] if return_blasst_stats else []) + ([dbg] if return_debug else [])
     return out[0] if len(out) == 1 else tuple(out)
+
+
+def prepare_qkv(q, k, v, cfg):
+    """``pipeline.py:42-110``: returns a dict with the fields of PreparedQKV
+    (codes as uint8, scales, qm, k_mean, correction (B, G, H, S) fp32 before
+    the cast to ``cfg.correction_dtype``, the k-means result)."""
+    q_work, k_work, v_work = q.contiguous(), k.contiguous(), v.contiguous()
+    km = None
+    if cfg.q_kmeans_k is not None:
+        km = okm.kmeans_reorder_tokens(q_work, n_clusters=cfg.q_kmeans_k, max_iters=cfg.q_kmeans_iters,
+                                       seed=cfg.q_kmeans_seed)
+        q_work = km["tensor_reordered"]
+    qm = k_mean = corr = None
+    if cfg.smoothing == "k_only":
+        k_work, k_mean = opre.smooth_k(k_work)
+    elif cfg.smoothing == "full":
+        k_work, k_mean = opre.smooth_k(k_work)
+        q_work, qm = opre.group_mean_q(q_work, block_q=cfg.q_smooth_block_size)
+        corr = torch.einsum("bqhd,bshd->bqhs", qm.double(), k_work.double())   # exact-ish; fp32 in the reference
+    elif cfg.smoothing != "off":
+        raise ValueError(f"unsupported smoothing mode: {cfg.smoothing!r}")
+    if cfg.qk_hadamard:
+        q_work, k_work = ohad.apply_qk_hadamard(q_work, k_work, random_sign=cfg.qk_hadamard_random_sign,
+                                                seed=cfg.qk_hadamard_seed)
+    qc, qs, _ = quant_qk(q_work, cfg)
+    kc, ks, _ = quant_qk(k_work, cfg)
+    vc, vs, _ = quant_v(v_work, cfg)
+    return {"q": qc, "k": kc, "v": vc, "q_scale": qs, "k_scale": ks, "v_scale": vs, "qm": qm, "k_mean": k_mean,
+            "correction": corr, "kmeans": km}

@@ -143,6 +143,17 @@ def test_hook_self_attention_matches_padded_call(gpu):
     assert out.shape == q.shape and torch.equal(out, ref)
     rec = wan_hook.get_call_log()[0]
     assert rec["kind"] == "self-fq" and rec["pad"] == 180
+    # against the oracle: pad, the reference algorithm (replayed on the kernel's
+    # scores: strict; and with its own scores: cosine), slice
+    # (bench/wan_attention_hook.py:249-294)
+    import parity
+    from oracle import pipeline as opipe
+    qc, kc, vc = (t.cpu() for t in (qp, kp, vp))
+    ops, sm = parity.kernel_operands(qc, kc, vc, cfg, gpu)
+    rep, dbg = parity.replay(qc, kc, vc, cfg, ops, parity.kernel_scores(ops, cfg, sm))
+    parity.strict_check(out.cpu(), rep[:, :n], "hook", allowance=dbg["flip_allowance_nhd"][:, :n])
+    oref = opipe.fake_quant_attention(qc, kc, vc, cfg)[:, :n]
+    assert parity.cosine(out.cpu(), oref) >= parity.COS_MIN
 
 
 @pytest.mark.gpu
