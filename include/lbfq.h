@@ -108,6 +108,17 @@ int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64
                 uint64_t seed, void* workspace, int32_t* labels, int32_t* order, int32_t* inverse,
                 lbfq_stream_t stream);
 
+/* Allocation-free lbfq_kmeans (no counterpart in the reference): for callers
+ * that cannot allocate device memory -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Same kernels and results
+ * as lbfq_kmeans; the workspace is a built-in device array of
+ * lbfq_kmeans_noalloc_max_workspace_bytes() (64 MiB) per GPU, held until the
+ * process ends.  Returns -1 when lbfq_kmeans_workspace_bytes() exceeds it.
+ * Calls that overlap on one GPU share that array and race. */
+int64_t lbfq_kmeans_noalloc_max_workspace_bytes(void);
+int lbfq_kmeans_noalloc(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int K, int iters,
+                        uint64_t seed, int32_t* labels, int32_t* order, int32_t* inverse, lbfq_stream_t stream);
+
 /* ---- qm_k row-max estimate + qm correction table --------------------------
  * Replaces attention.py:366-395 (_estimate_rowmax_from_qm_k) and precomputes
  * the kernel's qm correction attention_triton.py:156-160:

@@ -11,6 +11,7 @@
 //            order, c = (float)(sum / count), empty clusters keep c;
 //   labels : those of the last assign of `iters` rounds.
 // The order is a stable counting sort of the labels (argsort stable=True).
+#include <mutex>
 #include "lbfq_common.h"
 #include "../../include/lbfq.h"
 
@@ -335,4 +336,56 @@ extern "C" int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64
                      inverse);
   LBFQ_LAUNCH_CHECK("km_sort");
   return 0;
+}
+
+// ---- allocation-free variant -------------------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph capture,
+// serving loops, harnesses that forbid hipMalloc): the workspace is a
+// file-scope device array, one copy per GPU, held until the process ends.
+// Its device address is looked up once per device (hipGetSymbolAddress, with
+// that device current) and kept; host code never uses the array's name as an
+// address.  Calls that overlap on one GPU share the array and race.  The
+// kernels write every workspace word they read, so nothing is cleared.
+constexpr int64_t kKmScratchBytes = int64_t{64} << 20;  // 64 MiB: the 14B Q k-means (40 x 32768, K=32) needs 43 MB
+static __device__ __align__(256) uint8_t scratch[kKmScratchBytes];
+namespace {
+constexpr int kMaxDevices = 64;
+void* g_km_scratch[kMaxDevices] = {};
+std::mutex g_km_scratch_mu;
+
+int km_scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  LBFQ_CHECK_ARG(e == hipSuccess, "lbfq_kmeans_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  LBFQ_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "lbfq_kmeans_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_km_scratch_mu);
+  if (!g_km_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      lbfq_set_error("lbfq_kmeans_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return -2;
+    }
+    g_km_scratch[dev] = p;
+  }
+  *out = g_km_scratch[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int64_t lbfq_kmeans_noalloc_max_workspace_bytes(void) { return kKmScratchBytes; }
+
+extern "C" int lbfq_kmeans_noalloc(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int K,
+                                   int iters, uint64_t seed, int32_t* labels, int32_t* order, int32_t* inverse,
+                                   lbfq_stream_t stream) {
+  LBFQ_CHECK_ARG(B > 0 && S > 0 && H > 0 && D > 0 && K > 0, "lbfq_kmeans_noalloc: empty shape");
+  const int64_t need = lbfq_kmeans_workspace_bytes(B, S, H, D, K);
+  LBFQ_CHECK_ARG(need <= kKmScratchBytes,
+                 "lbfq_kmeans_noalloc: the problem needs %lld bytes of workspace, above the %lld-byte built-in "
+                 "scratch; use lbfq_kmeans with a caller workspace",
+                 (long long)need, (long long)kKmScratchBytes);
+  void* ws = nullptr;
+  const int rc = km_scratch_ptr(&ws);
+  if (rc) return rc;
+  return lbfq_kmeans(x, dtype, B, S, H, D, K, iters, seed, ws, labels, order, inverse, stream);
 }

@@ -127,6 +127,9 @@ _SIGS = {
     "lbfq_kmeans_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "lbfq_kmeans": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, ctypes.c_uint64, _vp, _vp, _vp, _vp,
                            _vp]),
+    "lbfq_kmeans_noalloc_max_workspace_bytes": (_i64, []),
+    "lbfq_kmeans_noalloc": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, ctypes.c_uint64, _vp, _vp, _vp,
+                                   _vp]),
     "lbfq_qmk": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
     "lbfq_qmk_kquant": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _vp,
                                _vp, _i64, _vp, _i64, _vp]),
