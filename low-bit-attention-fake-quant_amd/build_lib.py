@@ -5,7 +5,7 @@ then linked into ``low_bit_fake_quant/liblbfq_hip.so`` (in-tree, next to the
 Python package that loads it).  The prepass / k-means translation units are
 compiled with ``-ffp-contract=off`` so their arithmetic is exactly the
 documented op sequence (the CPU oracle reproduces it bit for bit); the
-attention unit allows contraction.  Packed-FP32 instructions are disabled
+attention units allow contraction and are built with -fno-honor-nans.  Packed-FP32 instructions are disabled
 for all device code.
 """
 
@@ -28,16 +28,21 @@ COMMON = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
+# The attention units: no NaN ever flows through their arithmetic (scores are
+# finite or -inf; the one 0/0 of BLASST's all-skipped zero-fill rows is formed
+# in the epilogue and only converted to the output dtype by hardware), so
+# fmaxf lowers to plain v_max / v_max3 without canonicalising its inputs.
+ATTN_FLAGS = ["-fno-honor-nans"]
 UNITS = {
     "lbfq_prepass.hip": ["-ffp-contract=off"],
     "lbfq_kmeans.hip": ["-ffp-contract=off"],
     "lbfq_qmk.hip": ["-ffp-contract=off"],
     "lbfq_probe.hip": ["-ffp-contract=off"],
     "lbfq_blasst_sim.hip": ["-ffp-contract=off"],
-    "lbfq_attn.hip": [],
-    "lbfq_attn_p0.hip": [],
-    "lbfq_attn_p1.hip": [],
-    "lbfq_attn_p2.hip": [],
+    "lbfq_attn.hip": ATTN_FLAGS,
+    "lbfq_attn_p0.hip": ATTN_FLAGS,
+    "lbfq_attn_p1.hip": ATTN_FLAGS,
+    "lbfq_attn_p2.hip": ATTN_FLAGS,
 }
 
 

@@ -8,8 +8,8 @@
 //
 // Work decomposition: one workgroup = 4 waves = 128 queries of one (b, h);
 // each wave owns 32 queries.  K and V^T tiles of 64 keys (== the reference
-// block_n) are copied global -> LDS directly (three-slot K ring, four-slot
-// V^T ring, staged three and two tiles ahead) together with the per-tile
+// block_n) are copied global -> LDS directly (four-slot K and V^T rings,
+// staged three and two tiles ahead) together with the per-tile
 // metadata (qm correction row, K/V scales, V block means), and shared by the
 // 4 waves.  Scores are computed transposed, S^T = K Q^T, so every lane owns
 // exactly one query: lane l holds query l % 32 and, in lane group
@@ -462,10 +462,13 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   constexpr bool HAS_BIAS = RB != RB_ONLINE;
   constexpr bool HAS_EST = RB == RB_EST_BIAS;
 
-  // rings: K tile i lives in slot i % 3, V^T tile i in slot i % 4
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[3][kTN * D];   // swizzled K rows (key order kperm)
+  // rings: K tile i lives in slot i % 4, V^T tile i in slot i % 4 (76 KB at
+  // D = 128, so two workgroups share a CU).  The main loop runs four tile steps
+  // per iteration, so every slot index is a compile-time constant there and
+  // the LDS addresses are immediate offsets.
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds[4][kTN * D];   // swizzled K rows (key order kperm)
   __shared__ __attribute__((aligned(16))) uint8_t v_lds[4][D * kTN];   // swizzled V^T rows
-  __shared__ __attribute__((aligned(16))) KMeta kmeta[3];
+  __shared__ __attribute__((aligned(16))) KMeta kmeta[4];
   __shared__ __attribute__((aligned(16))) VMeta<D> vmeta[4];
   __shared__ __attribute__((aligned(16))) float binit[HAS_BIAS ? kWaves : 1][2][kTN];  // bias / C per query half
 
@@ -755,7 +758,6 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   // have already consumed (block 0) or after chunk 3 (block 1).  The
   // accumulator rescale for tile it closes the step, so the PV of tile it in
   // the next step accumulates into it directly.
-  int slot = 0;       // K slot of tile it (tile i in slot i % 3); V^T slot: tile i in slot i % 4
   v8i pop_prev;       // P codes of tile it-1 (zero codes before the first tile)
   int pe_prev = 127;  // their E8M0 scale (MX P)
   float fcq[BL == 3 ? 32 : 1];  // UTA fill, 32/64 bins: fill codes of the lane's keys (current where the row skips)
@@ -770,17 +772,18 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   // MASKED: the tile holds keys >= S (only the last tile, when S % 64 != 0);
   // the body is instantiated with and without the masking so the common tiles
   // carry no merge of masked and unmasked scores
-  auto step = [&](const int it, auto masked_tag) __attribute__((always_inline)) {
+  // ph = it % 4, passed as a literal in the unrolled main loop
+  auto step = [&](const int it, auto masked_tag, const int ph) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
-    const int cur = slot, nxt = slot == 2 ? 0 : slot + 1;
-    const int vprev = (it - 1) & 3, vcur = it & 3;
+    const int nxt = (ph + 1) & 3;          // K slot of tile it+1
+    const int vprev = (ph + 3) & 3, vcur = ph;
     const int key0 = it * kTN;
-    // global -> LDS prefetch: K of tile it+3 into the slot of tile it (read in
-    // the previous step), V^T and metadata of tile it+2 into the slot of tile
-    // it-2 (clamped: the last iterations reload the last tile into slots
-    // nobody reads any more)
-    load_k(it + 3 < nt ? it + 3 : nt - 1, cur);
-    load_v(it + 2 < nt ? it + 2 : nt - 1, (it + 2) & 3);
+    // global -> LDS prefetch: K of tile it+3 into the slot of tile it-1 (read
+    // two steps ago), V^T and metadata of tile it+2 into the slot of tile it-2
+    // (clamped: the last iterations reload the last tile into slots nobody
+    // reads any more)
+    load_k(it + 3 < nt ? it + 3 : nt - 1, (ph + 3) & 3);
+    load_v(it + 2 < nt ? it + 2 : nt - 1, (ph + 2) & 3);
 
     // ---- scores: sv = dot + bias / C; the log2-unit score is u = sv * C ----------
     const float Ct[2] = {Ct_next[0], Ct_next[1]};
@@ -840,8 +843,13 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       m_new = skip ? m2 : mij;
       skipped += skip ? 1.0f : 0.0f;  // branch-free; the g == 0 lanes' counts are written
     } else if constexpr (HAS_EST && P_MODE == 2) {
-      // branch-free: without dyn_est, m2 stays at the estimate (adjust is false)
-      const bool lzero = xor32_add(l) == 0.0f;  // l >= 0 in both halves
+      // branch-free: without dyn_est, m2 stays at the estimate (adjust is false).
+      // l == 0 (no mass accumulated, attention_triton.py:200-207) holds exactly
+      // before the first tile: every branch below leaves the tile's largest P at
+      // code 448 (ra = 2^(bmax - m_new) >= 2^-32 since `over` fires beyond 32),
+      // so l > 0 afterwards -- unless all of a row's scores sit ~197 log2 units
+      // under its m, where the reference's fp32 exp2 underflows to 0 as well.
+      const bool lzero = it == 0;
       const float ms = hmax(max_seen, bmax);
       const bool under = (bmax - m2) > 16.0f;
       const bool over = (m2 - ms) > 32.0f;
@@ -938,8 +946,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       __builtin_amdgcn_sched_barrier(0);
-      float Tc = T;
-      pin(Tc);
+      const float Tc = T;
       // matrix work of chunk c: PV block c of tile it-1, QK MFMAs of block 0 of
       // tile it+1 (its scores were consumed by chunks 0-1)
       if (c < NDB) {
@@ -1066,20 +1073,22 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     }
 
     lds_publish<kCopies>();
-    slot = nxt;
   };
   const int nfull = (S % kTN) ? nt - 1 : nt;
   {
-    // two steps per iteration: the loop-carried scores, P codes and ring state
-    // alternate between two register sets instead of being copied at the back edge
+    // four steps per iteration: ring slots are constants, and the loop-carried
+    // scores, P codes and scale registers rotate through the unrolled steps
+    // instead of being copied at the back edge
     int it0 = 0;
-    for (; it0 + 1 < nfull; it0 += 2) {
-      step(it0, std::false_type{});
-      step(it0 + 1, std::false_type{});
+    for (; it0 + 3 < nfull; it0 += 4) {
+      step(it0, std::false_type{}, 0);
+      step(it0 + 1, std::false_type{}, 1);
+      step(it0 + 2, std::false_type{}, 2);
+      step(it0 + 3, std::false_type{}, 3);
     }
-    if (it0 < nfull) step(it0, std::false_type{});
+    for (; it0 < nfull; ++it0) step(it0, std::false_type{}, it0 & 3);
   }
-  if (nfull < nt) step(nt - 1, std::true_type{});
+  if (nfull < nt) step(nt - 1, std::true_type{}, (nt - 1) & 3);
   if constexpr (QK_MX) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
