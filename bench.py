@@ -14,7 +14,11 @@ N).  The prepass kernels (quantisers, qm.K_s, k-means) are timed separately
 and reported in GB/s; the whole fake_quant_attention call with cached
 preprocess is reported as ``e2e_cached``.  ``cpu_baseline`` times the CPU
 oracle's attention on one head and a bounded row sample; the same sample
-gives the error of the GPU output against the oracle at full size.
+gives the error of the GPU output against the oracle at full size, both
+against the reference (its own bf16-dequant scores) and against the
+reference algorithm replayed on the kernel's scores.  With the default
+config the attention of BASELINE configs 1, 3 and 4 is timed in the same run
+(``other_configs``; config 4's BLASST skip rate included).
 """
 
 from __future__ import annotations
@@ -62,7 +66,8 @@ def cpu_baseline_and_error(q, k, v, cfg, out_gpu, n_real, rows_sample, sm_scale)
     the P-requant path -- quantise the head, row-max estimate, streaming
     attention -- for a bounded sample of query rows (timed; the reference's
     timing likewise includes quant/dequant and excludes the cached preprocess,
-    bench/eval_wan21.py:208-255).  Returns (cpu_baseline dict, error dict)."""
+    bench/eval_wan21.py:208-255).  Returns (cpu_baseline dict, error dict,
+    error against the replay on the kernel's scores)."""
     from oracle import pipeline as opipe
     q0, k0, v0 = (t[:, :, :1].contiguous() for t in (q, k, v))
     b, s, h, d = q0.shape
@@ -93,7 +98,70 @@ def cpu_baseline_and_error(q, k, v, cfg, out_gpu, n_real, rows_sample, sm_scale)
            "max_abs_beyond_1_bf16_ulp": (diff - ulp).clamp_min(0).max().item(),
            "frac_gt_1e-2": (diff > 1e-2).float().mean().item(), "rows": len(rows), "head": 0,
            "vs": "CPU oracle of the reference path (not SDPA)"}
-    return cpu, err
+    log("error against the replay on the kernel's scores ...")
+    err_replay = replay_error(q, k, v, cfg, sm_scale, out_gpu, n_real, min(rows_sample, 2048))
+    return cpu, err, err_replay
+
+
+def replay_error(q, k, v, cfg, sm_scale, out_gpu, n_real, rows_sample):
+    """Part of the cpu_baseline leg (the oracle as checker): the GPU output
+    against the oracle's reference algorithm replayed on the kernel's own
+    scores (tests/parity.py), for head 0 and a row sample -- the strict part of
+    the parity check at full size (untimed)."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import parity
+    from oracle import pipeline as opipe
+    q0, k0, v0 = (t[:, :, :1].contiguous() for t in (q, k, v))
+    ops0, _ = parity.kernel_operands(q0, k0, v0, cfg, torch.device("cuda:0"), sm_scale)
+    qw, kw, vw, qm, v_alpha, q_km, _ = opipe.preprocess(q0, k0, v0, cfg)
+    order = q_km["order"][0] if q_km is not None else torch.arange(q0.shape[1])
+    gen = torch.Generator().manual_seed(1)
+    cand = torch.nonzero(order < n_real).flatten()
+    rows = cand[torch.randperm(len(cand), generator=gen)[:rows_sample]].sort().values
+    u = parity.kernel_scores(ops0, cfg, sm_scale, rows=rows.to(torch.int32))
+    rm = ops0.rowmax.cpu() if ops0.rowmax is not None else None
+    rep, dbg = opipe.p_requant_path(qw, kw, vw, qm, v_alpha, cfg, sm_scale, torch.float32, rows=rows,
+                                    scores_log2=u, rowmax_log2=rm, return_debug=True)
+    got = out_gpu[0, order[rows], 0].float().cpu()
+    want = rep[0, :, 0].float()
+    d = (got - want).abs()
+    tol = parity.tolerance(want) + dbg["flip_allowance"][0, 0].float()
+    return {"cos": parity.cosine(got, want), "max_abs": d.max().item(),
+            "elements_beyond_tolerance": int((d > tol).sum()), "rows": len(rows), "head": 0,
+            "vs": "the reference algorithm replayed on the kernel's own scores (strict parity)"}
+
+
+def other_configs(configs, dev, steps: int = 5):
+    """Attention time of the other BASELINE configs in the same run (inputs,
+    preprocess and quantisation untimed), and config 4's BLASST skip rate."""
+    from low_bit_fake_quant.attention import _lazy_preprocess, quantize_operands
+    from low_bit_fake_quant.attention_kernel import attention_flops, launch_attention
+    from low_bit_fake_quant.wan import make_inputs, pad_qkv, workloads
+    res = {}
+    for c in configs:
+        w = workloads()[c]
+        cfg = w.cfg
+        q, k, v = make_inputs(w, seed=0)
+        q, k, v, n = pad_qkv(q, k, v, cfg)
+        qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+        del q, k, v
+        sm = 1.0 / (w.D ** 0.5)
+        ops = quantize_operands(_lazy_preprocess(qd, kd, vd, cfg), cfg, sm)
+        del qd, kd, vd
+        ms = _events_time(lambda: launch_attention(ops, cfg, sm, torch.bfloat16), steps, 3)
+        fl = attention_flops(n, w.H, w.D)
+        r = {"workload": w.name, "ms": ms, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+             "frac_of_fp8_peak": fl / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS}
+        if cfg.blasst_lambda is not None:
+            _, stats = launch_attention(ops, cfg, sm, torch.bfloat16, return_blasst_stats=True)
+            st = stats.sum(dim=(0, 1))
+            r.update({"blasst_lambda": cfg.blasst_lambda, "blasst_fill": cfg.blasst_fill,
+                      "skip_rate": (st[0] / st[1]).item(), "TFLOPs_note": "dense-equivalent (4 N^2 D H)"})
+        log(f"config {c}: {ms:.3f} ms/launch, {r['TFLOPs']:.1f} TFLOP/s")
+        res[str(c)] = r
+        del ops
+        torch.cuda.empty_cache()
+    return res
 
 
 def traffic_from_profile(config: int):
@@ -118,6 +186,8 @@ def main() -> int:
     ap.add_argument("--heads", type=int, default=0, help="override H (debug)")
     ap.add_argument("--cpu-rows", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip timing configs 1, 3 and 4 beside the headline config")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="driver for rocprofv3 --pmc passes: a 1 GiB calibration copy, then one attention launch")
     args = ap.parse_args()
@@ -233,10 +303,16 @@ def main() -> int:
     prepass["frac_of_hbm_peak"] = prepass["quantise_qmk_GBps"] / HBM_PEAK_GBS
 
     cpu_baseline = None
-    err = None
+    err = err_replay = None
     if not args.no_cpu and args.config in (1, 2, 3):
         log("cpu baseline / error sample ...")
-        cpu_baseline, err = cpu_baseline_and_error(q, k, v, cfg, out, n_real, args.cpu_rows, sm_scale)
+        cpu_baseline, err, err_replay = cpu_baseline_and_error(q, k, v, cfg, out, n_real, args.cpu_rows,
+                                                               sm_scale)
+    others = None
+    if not args.no_other_configs and args.heads == 0 and args.config == 2:
+        del qd, kd, vd, ops, prep
+        torch.cuda.empty_cache()
+        others = other_configs([1, 3, 4], dev)
 
     roof = {"bound": "mfma", "achieved": tflops, "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": tflops / FP8_PEAK_TFLOPS, "traffic": None,
@@ -266,6 +342,8 @@ def main() -> int:
         "e2e_cached_TFLOPs": flops / (e2e_ms * 1e-3) / 1e12,
         "full_call_ms": full_ms,
         "err_vs_oracle": err,
+        "err_vs_replay": err_replay,
+        "other_configs": others,
         "next_to_path": extra,
     }
     print(json.dumps(line))

@@ -466,11 +466,22 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   // D = 128, so two workgroups share a CU).  The main loop runs four tile steps
   // per iteration, so every slot index is a compile-time constant there and
   // the LDS addresses are immediate offsets.
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[4][kTN * D];   // swizzled K rows (key order kperm)
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[4][D * kTN];   // swizzled V^T rows
-  __shared__ __attribute__((aligned(16))) KMeta kmeta[4];
-  __shared__ __attribute__((aligned(16))) VMeta<D> vmeta[4];
-  __shared__ __attribute__((aligned(16))) float binit[HAS_BIAS ? kWaves : 1][2][kTN];  // bias / C per query half
+  // One ordered block: the small per-tile tables first, so that every access
+  // to them is a base register plus a 16-bit immediate offset (ds_read /
+  // ds_write offsets stop at 64 KB), then the rings.
+  struct __attribute__((aligned(16))) Smem {
+    float binit[HAS_BIAS ? kWaves : 1][2][kTN];  // bias / C per query half
+    KMeta kmeta[4];
+    VMeta<D> vmeta[4];
+    uint8_t k_lds[4][kTN * D];  // swizzled K rows (key order kperm)
+    uint8_t v_lds[4][D * kTN];  // swizzled V^T rows
+  };
+  __shared__ Smem smem;
+  auto& binit = smem.binit;
+  auto& kmeta = smem.kmeta;
+  auto& vmeta = smem.vmeta;
+  auto& k_lds = smem.k_lds;
+  auto& v_lds = smem.v_lds;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
