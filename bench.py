@@ -24,6 +24,7 @@ config the attention of BASELINE configs 1, 3 and 4 is timed in the same run
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -153,10 +154,23 @@ def other_configs(configs, dev, steps: int = 5):
         r = {"workload": w.name, "ms": ms, "TFLOPs": fl / (ms * 1e-3) / 1e12,
              "frac_of_fp8_peak": fl / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS}
         if cfg.blasst_lambda is not None:
-            _, stats = launch_attention(ops, cfg, sm, torch.bfloat16, return_blasst_stats=True)
+            _, stats, wt = launch_attention(ops, cfg, sm, torch.bfloat16, return_blasst_stats=True,
+                                            return_wave_tiles=True)
             st = stats.sum(dim=(0, 1))
+            nt = (n + 63) // 64
+            wave_tiles = wt.shape[0] * wt.shape[1] * nt
+            w_all = wt[..., 0].sum().item() / wave_tiles
             r.update({"blasst_lambda": cfg.blasst_lambda, "blasst_fill": cfg.blasst_fill,
-                      "skip_rate": (st[0] / st[1]).item(), "TFLOPs_note": "dense-equivalent (4 N^2 D H)"})
+                      "skip_rate": (st[0] / st[1]).item(), "TFLOPs_note": "dense-equivalent (4 N^2 D H)",
+                      # (wave of 32 rows, 64-key tile) pairs: every row skipped (the softmax is
+                      # elided) / some row skipped
+                      "wave_tiles_all_skipped": w_all,
+                      "wave_tiles_some_skipped": wt[..., 1].sum().item() / wave_tiles})
+            if cfg.blasst_fill == "mean_a1.5":  # the second fill BASELINE names (same decisions)
+                cu = dataclasses.replace(cfg, blasst_fill="uta16_a1.5")
+                ms_u = _events_time(lambda: launch_attention(ops, cu, sm, torch.bfloat16), steps, 3)
+                r["uta16_a1.5"] = {"ms": ms_u, "TFLOPs": fl / (ms_u * 1e-3) / 1e12}
+                log(f"config {c} uta16_a1.5: {ms_u:.3f} ms/launch")
         log(f"config {c}: {ms:.3f} ms/launch, {r['TFLOPs']:.1f} TFLOP/s")
         res[str(c)] = r
         del ops

@@ -183,9 +183,29 @@ typedef struct {
   float* blasst_row_skips;        /* (B*H, S) fp32 in output-row order: K blocks each */
                                   /* row skipped (the per-row decisions behind the  */
                                   /* stats, attention_triton.py:165-175), or NULL   */
+  int32_t* blasst_wave_tiles;     /* (B*H, ceil(S/128)*4, 2) int32, or NULL: per    */
+                                  /* wave of 32 reordered query rows, the 64-key    */
+                                  /* tiles every row of it skipped and the tiles    */
+                                  /* some row of it skipped                         */
+  const float* v_tile_colsum;     /* (B*H, s_pitch/64, D) from lbfq_v_tile_colsum, */
+                                  /* or NULL.  With a per-row BLASST fill (not uta) */
+                                  /* and no V smoothing, a full tile that all 32    */
+                                  /* rows of a wave skip is applied as fill x these */
+                                  /* sums instead of its PV MFMAs                   */
 } lbfq_attn_params;
 
 int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t stream);
+
+/* Column sums of the V^T codes (B*H, D, s_pitch) over each 64-key tile, for
+ * lbfq_attn_params.v_tile_colsum: colsum (B*H, s_pitch/64, D) fp32 =
+ * sum over the tile's keys k < S of decode(code[d][k]), times 2^(e - 127)
+ * with e the E8M0 scale of (block of k, d) for MX V (v_kind 2; v_scale as in
+ * lbfq_attn_params).  No counterpart in the reference: it supports the skip
+ * of PV work that BLASST decides (attention_triton.py:165-175) -- when every
+ * key of a row carries the same fill p, that row's PV product is p times
+ * these sums. */
+int lbfq_v_tile_colsum(const uint8_t* v_codes_t, int64_t BH, int64_t S, int64_t s_pitch, int64_t D, int v_kind,
+                       const void* v_scale, int v_block, float* colsum, lbfq_stream_t stream);
 
 /* Scores of lbfq_attention_fwd's K-loop in log2 units, u = (Q K^T * sm_scale +
  * the qm correction) * log2(e), formed exactly as the kernel forms them (same

@@ -108,6 +108,8 @@ int make_kargs(const lbfq_attn_params* p, KArgs& a, const char* who) {
   a.v_alpha = p->v_alpha;
   a.stats = p->blasst_stats;
   a.row_skips = p->blasst_row_skips;
+  a.wave_tiles = p->blasst_wave_tiles;
+  a.vcol = p->v_tile_colsum;
   a.out = p->out;
   a.out_dtype = p->out_dtype;
   a.out_row_map = p->out_row_map;
@@ -188,7 +190,58 @@ __global__ void __launch_bounds__(64) attn_scores_kernel(const KArgs a, const in
   }
 }
 
+// Column sums of the V^T codes over each 64-key tile: colsum[bh][t][d] =
+// sum over keys k < S of tile t of decode(code[d][k]), times the E8M0 scale
+// of the (key block, d) pair for MX V (every tile lies inside one V block).
+// One thread per d reads the row's 64 contiguous bytes.
+__global__ void __launch_bounds__(128) v_colsum_kernel(const uint8_t* __restrict__ vt, int S, int P, int D,
+                                                       int v_mx, const uint8_t* __restrict__ ve, int lg_vblk,
+                                                       int nvblk, float* __restrict__ out) {
+  const int d = threadIdx.x, t = blockIdx.x, bh = blockIdx.y;
+  if (d >= D) return;
+  const int key0 = t * kTN;
+  const uint8_t* row = vt + (static_cast<size_t>(bh) * D + d) * P + key0;
+  const int nv = S - key0 < kTN ? S - key0 : kTN;
+  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < kTN / 16; ++c) {
+    const uint4 x = *reinterpret_cast<const uint4*>(row + 16 * c);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int k = 16 * c + 4 * q + b;
+        const float v = __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(w[q] >> (8 * b)), 0);
+        part[b] += k < nv ? v : 0.0f;
+      }
+  }
+  float sum = (part[0] + part[1]) + (part[2] + part[3]);
+  if (v_mx) sum = ldexpf(sum, static_cast<int>(ve[(static_cast<size_t>(bh) * nvblk + (key0 >> lg_vblk)) * D + d]) - 127);
+  out[(static_cast<size_t>(bh) * (P / kTN) + t) * D + d] = sum;
+}
+
 }  // namespace
+
+extern "C" int lbfq_v_tile_colsum(const uint8_t* v_codes_t, int64_t BH, int64_t S, int64_t s_pitch, int64_t D,
+                                  int v_kind, const void* v_scale, int v_block, float* colsum,
+                                  lbfq_stream_t stream) {
+  LBFQ_CHECK_ARG(v_codes_t && colsum && BH > 0 && S > 0, "lbfq_v_tile_colsum: bad arguments");
+  LBFQ_CHECK_ARG(D == 64 || D == 128, "lbfq_v_tile_colsum: D must be 64 or 128");
+  LBFQ_CHECK_ARG(s_pitch >= S && s_pitch % kTN == 0 && s_pitch < (int64_t{1} << 30),
+                 "lbfq_v_tile_colsum: s_pitch must be >= S and a multiple of %d", kTN);
+  LBFQ_CHECK_ARG(BH <= 65535, "lbfq_v_tile_colsum: too many heads");
+  LBFQ_CHECK_ARG(v_kind != 2 || (v_scale && v_block >= kTN && is_pow2(v_block) && S % v_block == 0),
+                 "lbfq_v_tile_colsum: MX V needs its scales and a block (power of two >= %d) dividing S", kTN);
+  const int mx = v_kind == 2;
+  dim3 grid(static_cast<unsigned>((S + kTN - 1) / kTN), static_cast<unsigned>(BH));
+  hipLaunchKernelGGL(v_colsum_kernel, grid, dim3(128), 0, static_cast<hipStream_t>(stream), v_codes_t,
+                     static_cast<int>(S), static_cast<int>(s_pitch), static_cast<int>(D), mx,
+                     reinterpret_cast<const uint8_t*>(v_scale), mx ? ilog2(v_block) : 0,
+                     mx ? static_cast<int>(S / v_block) : 1, colsum);
+  LBFQ_LAUNCH_CHECK("lbfq_v_tile_colsum");
+  return 0;
+}
 
 extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t stream) {
   KArgs a;

@@ -98,6 +98,8 @@ struct KArgs {
   const float* v_alpha;
   float* stats;
   float* row_skips;
+  int* wave_tiles;
+  const float* vcol;  // (B*H, P/64, D) V tile column sums, or null
   void* out;
   int out_dtype;
   const int32_t* out_row_map;
@@ -111,11 +113,12 @@ struct KMeta {
   float ksc[kTN];           // fp8_block: scale of the 16-key group of each key
 };
 
-template <int D>
+template <int D, bool COLSUM>
 struct VMeta {
   uint32_t ve[kTN];         // E8M0 byte of each V column (4 per word, D/4 words); 127 unless V is MX
   float valpha[D];          // V block mean of the tile
   float vsc[kTN];           // fp8_block V scale of the tile (all entries equal)
+  float vcol[COLSUM ? D : 1];  // sum over the tile's keys of each V column (codes, MX-scaled)
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -300,9 +303,26 @@ __device__ __forceinline__ float blasst_row_fill(const KArgs& a, const v16f (&sc
   if (fk == FILL_MAX) {
     f = max_bound * fa * rn;
   } else if (fk == FILL_MEAN || fk == FILL_LOGN) {
-    float s = 0.0f;
+    // the scores of a full tile are all finite: each 16-key group's sum is
+    // taken in accumulator units (pairwise) and scaled by its C once
+    float s;
+    if constexpr (MASKED) {
+      s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) s += valid_or(sc[j >> 4][j & 15] * Ct[j >> 4], 0.0f);
+      for (int j = 0; j < 32; ++j) s += valid_or(sc[j >> 4][j & 15] * Ct[j >> 4], 0.0f);
+    } else {
+      float h[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float p8[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) p8[r] = sc[t][r] + sc[t][r + 8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p8[r] += p8[r + 4];
+        h[t] = (p8[0] + p8[2]) + (p8[1] + p8[3]);
+      }
+      s = fmaf(h[0], Ct[0], h[1] * Ct[1]);
+    }
     const float mean = xor32_add(s) * rn;  // log2 units
     if (fk == FILL_MEAN) {
       f = fminf(fa * n * fast_exp2(mean - m_new + off), max_bound) * rn;
@@ -310,7 +330,8 @@ __device__ __forceinline__ float blasst_row_fill(const KArgs& a, const v16f (&sc
       float vs = 0.0f;
 #pragma unroll
       for (int j = 0; j < 32; ++j) {
-        const float c = valid_or(sc[j >> 4][j & 15] * Ct[j >> 4] - mean, 0.0f);
+        float c = fmaf(sc[j >> 4][j & 15], Ct[j >> 4], -mean);
+        if constexpr (MASKED) c = valid_or(c, 0.0f);
         vs = fmaf(c, c, vs);
       }
       const float var2 = xor32_add(vs) * rn;  // log2 units squared
@@ -334,64 +355,121 @@ __device__ __forceinline__ float blasst_row_fill(const KArgs& a, const v16f (&sc
 // uta_fill, with the scores read in place) and returns the row's largest;
 // uta_pack turns them into the lane's E4M3 fill codes, 4 keys per word in the
 // order of the P codes, and their sum in the order of the exact row sum.
-template <int BS>
+// In a full tile every bin holds its BS keys (a power of two), so a run's
+// scores are summed in accumulator units and scaled by its C once, the counts
+// cancel exactly (fa * cnt * x / cnt == fa * x), and a run's four-key words
+// share one code.
+template <int BS, bool MASKED>
 __device__ __forceinline__ float uta_runs(const v16f (&sc)[2], const float (&Ct)[2], float m_new, float off,
                                           float fa, float (&fr)[8]) {
   constexpr int RUN = BS <= 16 ? BS : 16;
   constexpr int NR = 32 / RUN;
-  static_assert(NR <= 8, "uta_runs: at most 8 runs per lane");
-  float s[NR], mx[NR], c[NR];
-#pragma unroll
-  for (int b = 0; b < NR; ++b) {
-    s[b] = 0.0f; mx[b] = -INFINITY; c[b] = 0.0f;
-#pragma unroll
-    for (int r = 0; r < RUN; ++r) {
-      const int j = RUN * b + r;
-      const float x = sc[j >> 4][j & 15] * Ct[j >> 4];
-      s[b] += valid_or(x, 0.0f);
-      mx[b] = hmax(mx[b], x);
-      c[b] += x != -INFINITY ? 1.0f : 0.0f;
-    }
-    if constexpr (BS >= 32) {
-      s[b] = xor32_add(s[b]);
-      mx[b] = xor32_max(mx[b]);
-      c[b] = xor32_add(c[b]);
-    }
-  }
-  if constexpr (BS == 64) {
-    s[0] += s[1]; mx[0] = hmax(mx[0], mx[1]); c[0] += c[1];
-    s[1] = s[0]; mx[1] = mx[0]; c[1] = c[0];
-  }
+  static_assert(NR <= 8 && RUN >= 4, "uta_runs: 4 to 16 keys per run");
   float fmx = 0.0f;
+  if constexpr (!MASKED) {
+    float s[NR], mx[NR];
 #pragma unroll
-  for (int b = 0; b < NR; ++b) {
-    const float sc_b = fmaxf(c[b], 1.0f), rc = __builtin_amdgcn_rcpf(sc_b);
-    const float f = fminf(fa * sc_b * fast_exp2(s[b] * rc - m_new + off), sc_b * fast_exp2(mx[b] - m_new + off)) * rc;
-    fmx = fmaxf(fmx, f);
-    fr[b] = f;
+    for (int b = 0; b < NR; ++b) {
+      const int t = (RUN * b) >> 4, r0 = (RUN * b) & 15;
+      float p[RUN / 2];
+#pragma unroll
+      for (int r = 0; r < RUN / 2; ++r) p[r] = sc[t][r0 + r] + sc[t][r0 + r + RUN / 2];
+#pragma unroll
+      for (int w = RUN / 4; w >= 1; w /= 2)
+#pragma unroll
+        for (int r = 0; r < w; ++r) p[r] += p[r + w];
+      float m = hmax(sc[t][r0], sc[t][r0 + 1]);
+#pragma unroll
+      for (int r = 2; r + 1 < RUN; r += 2) m = hmax3(m, sc[t][r0 + r], sc[t][r0 + r + 1]);
+      s[b] = p[0] * Ct[t];
+      mx[b] = m * Ct[t];  // C > 0
+      if constexpr (BS >= 32) {
+        s[b] = xor32_add(s[b]);
+        mx[b] = xor32_max(mx[b]);
+      }
+    }
+    if constexpr (BS == 64) {
+      s[0] += s[1]; mx[0] = hmax(mx[0], mx[1]);
+      s[1] = s[0]; mx[1] = mx[0];
+    }
+    constexpr float inv = 1.0f / BS;
+#pragma unroll
+    for (int b = 0; b < NR; ++b) {
+      const float f = fminf(fa * fast_exp2(s[b] * inv - m_new + off), fast_exp2(mx[b] - m_new + off));
+      fmx = fmaxf(fmx, f);
+      fr[b] = f;
+    }
+  } else {
+    float s[NR], mx[NR], c[NR];
+#pragma unroll
+    for (int b = 0; b < NR; ++b) {
+      s[b] = 0.0f; mx[b] = -INFINITY; c[b] = 0.0f;
+#pragma unroll
+      for (int r = 0; r < RUN; ++r) {
+        const int j = RUN * b + r;
+        const float x = sc[j >> 4][j & 15] * Ct[j >> 4];
+        s[b] += valid_or(x, 0.0f);
+        mx[b] = hmax(mx[b], x);
+        c[b] += x != -INFINITY ? 1.0f : 0.0f;
+      }
+      if constexpr (BS >= 32) {
+        s[b] = xor32_add(s[b]);
+        mx[b] = xor32_max(mx[b]);
+        c[b] = xor32_add(c[b]);
+      }
+    }
+    if constexpr (BS == 64) {
+      s[0] += s[1]; mx[0] = hmax(mx[0], mx[1]); c[0] += c[1];
+      s[1] = s[0]; mx[1] = mx[0]; c[1] = c[0];
+    }
+#pragma unroll
+    for (int b = 0; b < NR; ++b) {
+      const float sc_b = fmaxf(c[b], 1.0f), rc = __builtin_amdgcn_rcpf(sc_b);
+      const float f = fminf(fa * sc_b * fast_exp2(s[b] * rc - m_new + off), sc_b * fast_exp2(mx[b] - m_new + off)) * rc;
+      fmx = fmaxf(fmx, f);
+      fr[b] = f;
+    }
   }
   return xor32_max(fmx);
 }
 
-template <int BS, int P_MODE>
+template <int BS, int P_MODE, bool MASKED>
 __device__ __forceinline__ void uta_pack(const v16f (&sc)[2], const float (&fr)[8], float qmul_f, uint32_t (&fpk)[8],
                                          float& fsum) {
   constexpr int RUN = BS <= 16 ? BS : 16;
-  float s4[4];
+  constexpr int NR = 32 / RUN;
+  if constexpr (!MASKED) {
+    float v[NR];
+    uint32_t wd[NR];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 4 * q + i;
-      const float f = sc[j >> 4][j & 15] != -INFINITY ? fr[j / RUN] : 0.0f;
-      v[i] = P_MODE == 0 ? fminf(f, kFp8Max) : f * qmul_f;
-      s4[i] = q == 0 ? v[i] : s4[i] + v[i];
+    for (int b = 0; b < NR; ++b) {
+      v[b] = P_MODE == 0 ? fminf(fr[b], kFp8Max) : fr[b] * qmul_f;
+      const int w2 = __builtin_amdgcn_cvt_pk_fp8_f32(v[b], v[b], __float_as_int(v[b]), false);
+      wd[b] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v[b], v[b], w2, true));
     }
-    int wd = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], __float_as_int(v[0]), false);
-    fpk[q] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], wd, true));
+#pragma unroll
+    for (int q = 0; q < 8; ++q) fpk[q] = wd[(4 * q) / RUN];
+    float t = v[0];
+#pragma unroll
+    for (int b = 1; b < NR; ++b) t += v[b];
+    fsum = t * static_cast<float>(RUN);
+  } else {
+    float s4[4];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 4 * q + i;
+        const float f = sc[j >> 4][j & 15] != -INFINITY ? fr[j / RUN] : 0.0f;
+        v[i] = P_MODE == 0 ? fminf(f, kFp8Max) : f * qmul_f;
+        s4[i] = q == 0 ? v[i] : s4[i] + v[i];
+      }
+      int wd = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], __float_as_int(v[0]), false);
+      fpk[q] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], wd, true));
+    }
+    fsum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
   }
-  fsum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
 }
 
 template <int P_MODE>
@@ -456,6 +534,11 @@ __device__ __forceinline__ float blasst_fill(const KArgs& a, const float (&u)[32
 template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA>
 __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1 : 2) attn_fwd_kernel(const KArgs a) {
   constexpr bool BLASST = BL != 0;
+  // BLASST with one fill value per row and tile, without V smoothing: a tile
+  // that every row of the wave skips adds fill * (column sums of V) to the
+  // accumulator instead of running its four PV MFMAs
+  constexpr bool ELIDE = BL == 1 && !VALPHA;
+  using VM = VMeta<D, ELIDE>;
   constexpr int NH = D / 64;          // 64-wide contraction halves of D
   constexpr int NDB = D / 32;         // 32-row blocks of O^T
   constexpr int CPT = kTN * D / 16 / kThreads;  // 16-byte chunks per thread per K (and V) tile
@@ -472,7 +555,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   struct __attribute__((aligned(16))) Smem {
     float binit[HAS_BIAS ? kWaves : 1][2][kTN];  // bias / C per query half
     KMeta kmeta[4];
-    VMeta<D> vmeta[4];
+    VM vmeta[4];
     uint8_t k_lds[4][kTN * D];  // swizzled K rows (key order kperm)
     uint8_t v_lds[4][D * kTN];  // swizzled V^T rows
   };
@@ -540,11 +623,18 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   float max_seen = -INFINITY;
   float sigma = 1.0f;  // acc holds O^T / sigma
   float skipped = 0.0f;  // BLASST: tiles this row skipped
+  int wt_all = 0, wt_any = 0;  // BLASST: tiles every / some row of the wave skipped (wave-uniform)
   v16f acc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.0f;
+  // The accumulator must never be a known constant at a PV MFMA: with a
+  // constant-zero input (e.g. in a peeled first iteration) the compiler does
+  // not tie the MFMA's destination to it and may give the destination the
+  // register of the V scale operand, which the MFMA still reads.
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) pin(acc[db]);
   // V smoothing (attention_triton.py c = c * alpha + rowsum(P_deq) (x) alpha_v)
   // is folded into acc: the correction of a tile, rowsum(P_deq) / sigma (x)
   // alpha_v, is added in the same units as the tile's PV product, so the
@@ -584,9 +674,9 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   const uint32_t k_lds0 = lds_addr(&k_lds[0][0]), v_lds0 = lds_addr(&v_lds[0][0]);
   const uint32_t km0 = lds_addr(&kmeta[0]), vm0 = lds_addr(&vmeta[0]);
   constexpr uint32_t kKBuf = kTN * D, kVBuf = D * kTN;
-  constexpr uint32_t kKMeta = sizeof(KMeta), kVMeta = sizeof(VMeta<D>);
+  constexpr uint32_t kKMeta = sizeof(KMeta), kVMeta = sizeof(VM);
   const bool v_mx = a.v_kind == 2, v_blk = a.v_kind == 1;
-  constexpr int kCopies = 2 * CPT + (HAS_BIAS ? 1 : 0) + 2 + (VALPHA ? D / 64 : 0);
+  constexpr int kCopies = 2 * CPT + (HAS_BIAS ? 1 : 0) + 2 + (VALPHA ? D / 64 : 0) + (ELIDE ? D / 64 : 0);
   // per-lane byte offsets of the small tables (lanes past a table's end repeat it)
   const uint32_t ke_lofs = 4 * (lane & (kTN * (D / 32) / 4 - 1));
   const uint32_t ve_lofs = 4 * (lane & (D / 4 - 1));
@@ -621,11 +711,19 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     const int vblk = bh * a.nvblk + (key0 >> a.lg_vblk);
     const void* vsrc = v_mx ? static_cast<const void*>(reinterpret_cast<const uint32_t*>(a.v_scale) + vblk * (D / 4))
                             : static_cast<const void*>(reinterpret_cast<const float*>(a.v_scale) + (v_blk ? vblk : 0));
-    g2l4(vsrc, v_mx ? ve_lofs : 0u, vmb + (v_mx ? offsetof(VMeta<D>, ve) : offsetof(VMeta<D>, vsc)));
+    g2l4(vsrc, v_mx ? ve_lofs : 0u, vmb + (v_mx ? offsetof(VM, ve) : offsetof(VM, vsc)));
     if constexpr (VALPHA) {
       const float* va = a.v_alpha + (static_cast<size_t>(bh) * a.nvsb + (key0 >> a.lg_vsb)) * D;
 #pragma unroll
-      for (int c = 0; c < D / 64; ++c) g2l4(va + 64 * c, 4 * lane, vmb + offsetof(VMeta<D>, valpha) + 256 * c);
+      for (int c = 0; c < D / 64; ++c) g2l4(va + 64 * c, 4 * lane, vmb + offsetof(VM, valpha) + 256 * c);
+    }
+    if constexpr (ELIDE) {
+      // the tile's V column sums (without a table, an unused copy of the
+      // first D * 4 bytes of the head's V^T codes, so the copy count stays fixed)
+      const float* cs = a.vcol ? a.vcol + (static_cast<size_t>(bh) * (P / kTN) + it) * D
+                               : reinterpret_cast<const float*>(vbase);
+#pragma unroll
+      for (int c = 0; c < D / 64; ++c) g2l4(cs + 64 * c, 4 * lane, vmb + offsetof(VM, vcol) + 256 * c);
     }
   };
 
@@ -886,11 +984,11 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       if (any_skip) {
         if constexpr (BL == 2) {
           switch (kTN / a.uta_bins) {
-            case 4: fmax = uta_runs<4>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
-            case 8: fmax = uta_runs<8>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
-            case 16: fmax = uta_runs<16>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
-            case 32: fmax = uta_runs<32>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
-            default: fmax = uta_runs<64>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            case 4: fmax = uta_runs<4, MASKED>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            case 8: fmax = uta_runs<8, MASKED>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            case 16: fmax = uta_runs<16, MASKED>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            case 32: fmax = uta_runs<32, MASKED>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
+            default: fmax = uta_runs<64, MASKED>(sc, Ct, m_new, off, a.fill_alpha, fr); break;
           }
         } else if constexpr (BL == 3) {
           float u[32];
@@ -923,17 +1021,18 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       s_lp = rf * (1.0f / kFp8Max);
       T = (floored ? m_new + kLog2DynFloor : bmax) - kLog2Fp8Max;
       sig_p = s_lp;
-      if constexpr (BLASST) qmul_f = kFp8Max / rf;
+      if constexpr (BLASST) qmul_f = kFp8Max * __builtin_amdgcn_rcpf(rf);
     }
     float fq = 0.0f;  // row fill (BL 1) in code units
+    int fqw = 0;      // BL 1, full tiles: four E4M3 codes of fq (the codes of a skipped row)
     if constexpr (BL == 2) {
       if (any_skip) {
         switch (kTN / a.uta_bins) {
-          case 4: uta_pack<4, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
-          case 8: uta_pack<8, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
-          case 16: uta_pack<16, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
-          case 32: uta_pack<32, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
-          default: uta_pack<64, P_MODE>(sc, fr, qmul_f, fpk, fsum); break;
+          case 4: uta_pack<4, P_MODE, MASKED>(sc, fr, qmul_f, fpk, fsum); break;
+          case 8: uta_pack<8, P_MODE, MASKED>(sc, fr, qmul_f, fpk, fsum); break;
+          case 16: uta_pack<16, P_MODE, MASKED>(sc, fr, qmul_f, fpk, fsum); break;
+          case 32: uta_pack<32, P_MODE, MASKED>(sc, fr, qmul_f, fpk, fsum); break;
+          default: uta_pack<64, P_MODE, MASKED>(sc, fr, qmul_f, fpk, fsum); break;
         }
       }
     } else if constexpr (BL == 3) {
@@ -943,6 +1042,10 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       }
     } else if constexpr (BL == 1) {
       fq = P_MODE == 0 ? fminf(fmax, kFp8Max) : fmax * qmul_f;
+      if constexpr (!MASKED) {
+        fqw = __builtin_amdgcn_cvt_pk_fp8_f32(fq, fq, __float_as_int(fq), false);
+        fqw = __builtin_amdgcn_cvt_pk_fp8_f32(fq, fq, fqw, true);
+      }
     }
     (void)fq;
     (void)qmul_f;
@@ -952,6 +1055,10 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     float ps4[4];
     // BLASST: every row of the wave skips this (full) tile (wave-uniform)
     const bool skip_all = (BL == 1 || BL == 2) && !MASKED && __all(skip);
+    if constexpr (BLASST) {
+      wt_all += __all(skip) ? 1 : 0;
+      wt_any += any_skip ? 1 : 0;
+    }
     v16f bi1;
     v16f rsm;  // V smoothing: rowsum of the codes of tile it-1
 #pragma unroll
@@ -989,7 +1096,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
         pq[jj] = fast_exp2(fmaf(sv(j), Ct[j >> 4], -Tc));
         // fill codes of a skipped row (zero on the keys past S of the last tile)
         if constexpr (BL == 3) pq[jj] = skip ? fcq[j] : pq[jj];
-        if constexpr (BL == 1) pq[jj] = skip ? ((MASKED && sv(j) == -INFINITY) ? 0.0f : fq) : pq[jj];
+        if constexpr (BL == 1 && MASKED) pq[jj] = skip ? (sv(j) == -INFINITY ? 0.0f : fq) : pq[jj];
         ps4[j & 3] = j < 4 ? pq[jj] : ps4[j & 3] + pq[jj];
       }
       if constexpr (P_MODE == 0) {
@@ -1005,6 +1112,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
         int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2], pq[4 * h2 + 1], __float_as_int(pq[4 * h2]), false);
         pop[2 * c + h2] = __builtin_amdgcn_cvt_pk_fp8_f32(pq[4 * h2 + 2], pq[4 * h2 + 3], wd, true);
         if constexpr (BL == 2) pop[2 * c + h2] = skip ? static_cast<int>(fpk[2 * c + h2]) : pop[2 * c + h2];
+        if constexpr (BL == 1 && !MASKED) pop[2 * c + h2] = skip ? fqw : pop[2 * c + h2];
       }
       }
       // score block 0 is consumed: it receives the bias of tile it+1
@@ -1018,23 +1126,13 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (BL == 1 || BL == 2) {
-      if (skip_all) {  // the codes (and for BL 1 the row sum terms) of the fill, as the chunks form them
-        if constexpr (BL == 1) {
-          int wd = __builtin_amdgcn_cvt_pk_fp8_f32(fq, fq, __float_as_int(fq), false);
-          wd = __builtin_amdgcn_cvt_pk_fp8_f32(fq, fq, wd, true);
-          float s8 = fq;
+      if (skip_all) {  // the fill codes (the row sums of skipped rows are set below)
+        // (zero codes when the tile is elided: its PV product is added below,
+        // and the PV MFMAs of the next step add nothing for it)
 #pragma unroll
-          for (int i = 1; i < 8; ++i) s8 += fq;
+        for (int q = 0; q < 8; ++q) pop[q] = BL == 1 ? (ELIDE && a.vcol ? 0 : fqw) : static_cast<int>(fpk[q]);
 #pragma unroll
-          for (int q = 0; q < 8; ++q) pop[q] = wd;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) ps4[k] = s8;
-        } else {
-#pragma unroll
-          for (int q = 0; q < 8; ++q) pop[q] = static_cast<int>(fpk[q]);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) ps4[k] = 0.0f;  // the row sum is fsum
-        }
+        for (int k = 0; k < 4; ++k) ps4[k] = 0.0f;
       }
     }
     // score block 1 is consumed: QK MFMAs of tile it+1 from the bias init
@@ -1043,6 +1141,19 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     for (int i = NH + 1; i < NQK; ++i) sc[1] = qk_mfma(i, ka[i & 1], sc[1], ke_n[i]);
     float psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
     if constexpr (BL == 2) psum = skip ? fsum : psum;  // the fill codes' sum
+    if constexpr (BL == 1) {
+      // a skipped row sums its pre-quant fill over the valid keys
+      // (attention_triton.py:324-326); each lane of the pair holds 32 keys of
+      // the row (32 t + 16 g + r), so it adds the fill once per valid key of its own
+      float nvl = 32.0f;
+      if constexpr (MASKED) {
+        int c = 0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) c += min(max(S - key0 - 32 * t - 16 * g, 0), 16);
+        nvl = static_cast<float>(c);
+      }
+      psum = skip ? (P_MODE == 0 ? fmax : fmax * qmul_f) * nvl : psum;
+    }
     psum *= s_lp;  // sum of the pre-quant p
     l = l * alpha + psum;
 #undef sv
@@ -1051,7 +1162,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     // (added in this step), before this step's rescale ----------------------------
     if constexpr (VALPHA) {
       const float w = rsm[0] * vw_prev;
-      const VMeta<D>& vmp = vmeta[vprev];
+      const VM& vmp = vmeta[vprev];
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -1065,11 +1176,37 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     // scale): the PV of tile it, issued in the next step, accumulates on top ------
     float sig_new = sig_p;
     sig_new *= v_blk ? vsc : 1.0f;
-    const float rsig = __builtin_amdgcn_rcpf(sig_new);
-    const float f = alpha * sigma * rsig;
-    sigma = sig_new;
+    // ELIDE: every row of the wave skipped this full tile, so each row's P is
+    // one fill code on all 64 keys and the tile's PV product is that code times
+    // the column sums of V.  It is added here in fp32, in the units of the
+    // current sigma (alpha is 1 for a skipped row, so nothing is rescaled),
+    // and the tile's P codes are left at zero, so the PV MFMAs that the next
+    // step issues for it add nothing.  (Skipping those MFMAs with a branch,
+    // or with a second step variant, needs a loop-carried flag; the kernel
+    // then exceeds 256 VGPRs and spills.)
+    const bool elide = ELIDE && !MASKED && skip_all && a.vcol != nullptr;
+    // an elided tile keeps sigma (f = 1: no rescale)
+    const float sig_keep = elide ? sigma : sig_new;
+    const float rsig = __builtin_amdgcn_rcpf(sig_keep);
+    if (elide && a.fill_kind != FILL_ZERO) {
+      const float w = __builtin_amdgcn_cvt_f32_fp8(fqw, 0) * s_lp * (v_blk ? vsc : 1.0f) * rsig;
+      const VM& vmc = vmeta[vcur];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const float4 cs = *reinterpret_cast<const float4*>(&vmc.vcol[32 * db + 8 * r4 + 4 * g]);
+          acc[db][4 * r4 + 0] = fmaf(w, cs.x, acc[db][4 * r4 + 0]);
+          acc[db][4 * r4 + 1] = fmaf(w, cs.y, acc[db][4 * r4 + 1]);
+          acc[db][4 * r4 + 2] = fmaf(w, cs.z, acc[db][4 * r4 + 2]);
+          acc[db][4 * r4 + 3] = fmaf(w, cs.w, acc[db][4 * r4 + 3]);
+        }
+      }
+    }
+    const float f = elide ? 1.0f : alpha * sigma * rsig;
+    sigma = sig_keep;
     if constexpr (VALPHA) vw_prev = s_lp * rsig;  // rowsum(P_deq) / sigma per code unit
-    if (P_MODE == 2 || __any(f != 1.0f)) {
+    if ((P_MODE == 2 && !ELIDE) || __any(f != 1.0f)) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -1089,13 +1226,19 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   {
     // four steps per iteration: ring slots are constants, and the loop-carried
     // scores, P codes and scale registers rotate through the unrolled steps
-    // instead of being copied at the back edge
+    // instead of being copied at the back edge.  Kernels with BLASST or V
+    // smoothing carry more state through a step; unrolled, they need more
+    // than the 256 VGPRs of two waves per SIMD and spill inside the loop, so
+    // they run one step per iteration (ring slots then come from it % 4).
+    constexpr bool UNROLL = !BLASST && !VALPHA;
     int it0 = 0;
-    for (; it0 + 3 < nfull; it0 += 4) {
-      step(it0, std::false_type{}, 0);
-      step(it0 + 1, std::false_type{}, 1);
-      step(it0 + 2, std::false_type{}, 2);
-      step(it0 + 3, std::false_type{}, 3);
+    if constexpr (UNROLL) {
+      for (; it0 + 3 < nfull; it0 += 4) {
+        step(it0, std::false_type{}, 0);
+        step(it0 + 1, std::false_type{}, 1);
+        step(it0 + 2, std::false_type{}, 2);
+        step(it0 + 3, std::false_type{}, 3);
+      }
     }
     for (; it0 < nfull; ++it0) step(it0, std::false_type{}, it0 & 3);
   }
@@ -1132,6 +1275,13 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
       const int rb = qi / a.block_m;
       atomicAdd(a.stats + (static_cast<size_t>(rb) * (a.B * a.H) + bh) * 2 + 0, skipped);
       atomicAdd(a.stats + (static_cast<size_t>(rb) * (a.B * a.H) + bh) * 2 + 1, static_cast<float>(nt));  // tiles seen
+    }
+  }
+  if constexpr (BLASST) {
+    if (a.wave_tiles && lane == 0) {
+      int* wt = a.wave_tiles + (static_cast<size_t>(bh) * a.nqb * kWaves + qb * kWaves + wave) * 2;
+      wt[0] = wt_all;
+      wt[1] = wt_any;
     }
   }
   if (!qvalid) return;

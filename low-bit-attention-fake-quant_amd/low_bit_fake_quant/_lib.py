@@ -81,6 +81,8 @@ class AttnParams(ctypes.Structure):
         ("out", _vp), ("out_dtype", _i32),
         ("out_row_map", _vp),
         ("blasst_row_skips", _vp),
+        ("blasst_wave_tiles", _vp),
+        ("v_tile_colsum", _vp),
     ]
 
 
@@ -135,6 +137,7 @@ _SIGS = {
                                _vp, _i64, _vp, _i64, _vp]),
     "lbfq_attention_fwd": (_i32, [ctypes.POINTER(AttnParams), _vp]),
     "lbfq_attention_scores": (_i32, [ctypes.POINTER(AttnParams), _vp, _i64, _vp, _vp]),
+    "lbfq_v_tile_colsum": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _i32, _vp, _vp]),
     "lbfq_p_requant_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
                                    ctypes.c_double, _i32, _vp]),
     "lbfq_rowmax_count": (_i32, [ctypes.POINTER(RowmaxCountParams), _vp]),

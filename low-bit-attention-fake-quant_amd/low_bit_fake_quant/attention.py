@@ -32,7 +32,7 @@ import torch
 
 from . import _lib
 from ._ops import RowSource, channel_amax, colsum_mean, column_mean, hadamard_scale, qmk, round_up, rowtile
-from .attention_kernel import launch_attention, parse_blasst_fill, validate_kernel_config
+from .attention_kernel import launch_attention, parse_blasst_fill, v_tile_colsum, validate_kernel_config
 from .config import QuantConfig
 from .hadamard import apply_qk_hadamard, qk_signs_device
 from .kmeans import KMeansReorderResult, gather_rows, kmeans_labels, make_result
@@ -274,6 +274,7 @@ class QuantizedOperands:
     rowmax: Optional[torch.Tensor]        # (B,H,G) max_n bias (log2 units)
     v_alpha: Optional[torch.Tensor]       # (B,H,S/vsb,D) fp32 block means (/ channel V scale)
     out_row_map: Optional[torch.Tensor]   # (B*H,S) int32
+    v_colsum: Optional[torch.Tensor] = None  # (B*H,P/64,D) fp32 V tile column sums (BLASST PV skip)
 
 
 def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> QuantizedOperands:
@@ -313,9 +314,14 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
             # the kernel adds the V-smoothing correction into its accumulator,
             # which the per-channel V scales multiply at the end
             v_alpha = v_alpha / v_scale[:, :, None, :]
+    v_colsum = None
+    if cfg.blasst_lambda is not None and v_alpha is None:
+        # lets the kernel apply a tile that all rows of a wave skip as fill x column sums
+        v_colsum = v_tile_colsum(v_codes, v_scale, v_kind, v_block, s)
     return QuantizedOperands(b=b, s=s, h=h, d=d, P=P, q_codes=q_codes, q_scale=q_scale, k_codes=k_codes,
                              k_scale=k_scale, v_codes_t=v_codes, v_scale=v_scale, v_kind=v_kind, v_block=v_block,
-                             bias=bias, rowmax=rowmax, v_alpha=v_alpha, out_row_map=prep.q_order_i32())
+                             bias=bias, rowmax=rowmax, v_alpha=v_alpha, out_row_map=prep.q_order_i32(),
+                             v_colsum=v_colsum)
 
 
 def _p_requant_hip(prep: _Prep, cfg: QuantConfig, sm_scale: float, out_dtype: torch.dtype,

@@ -177,19 +177,35 @@ def _attn_params(ops, cfg, sm_scale: float) -> "_lib.AttnParams":
         p.blasst_lambda = 0.0
         p.blasst_fill, p.blasst_fill_alpha, p.blasst_uta_bins = 0, 1.0, 1
     p.out_row_map = _lib.ptr(ops.out_row_map)
+    p.v_tile_colsum = _lib.ptr(getattr(ops, "v_colsum", None))
     return p
 
 
+def v_tile_colsum(v_codes_t: torch.Tensor, v_scale: torch.Tensor, v_kind: int, v_block: int, s: int) -> torch.Tensor:
+    """Column sums of the V^T codes (B,H,D,P) over each 64-key tile (MX V:
+    scaled by its E8M0 block scales): (B*H, P/64, D) fp32."""
+    lib = _lib.load()
+    b, h, d, P = v_codes_t.shape
+    out = torch.empty((b * h, P // 64, d), dtype=torch.float32, device=v_codes_t.device)
+    _lib.check(lib.lbfq_v_tile_colsum(v_codes_t.data_ptr(), b * h, s, P, d, int(v_kind), v_scale.data_ptr(),
+                                      int(v_block), out.data_ptr(), _lib.stream_handle(v_codes_t.device)),
+               "lbfq_v_tile_colsum")
+    return out
+
+
 def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, return_blasst_stats: bool = False,
-                     return_row_skips: bool = False):
+                     return_row_skips: bool = False, return_wave_tiles: bool = False):
     """Run the attention kernel on quantised operands; returns NHD output, then
-    (when asked) the BLASST stats (ceil(S/block_m), B*H, 2) and the per-row
-    skipped K-block counts (B*H, S) in output-row order."""
+    (when asked) the BLASST stats (ceil(S/block_m), B*H, 2), the per-row
+    skipped K-block counts (B*H, S) in output-row order, and per wave of 32
+    reordered query rows the number of 64-key tiles that every row of the wave
+    skipped (softmax and PV elided) and that some row skipped,
+    (B*H, ceil(S/128)*4, 2) int32."""
     lib = _lib.load()
     dev = ops.q_codes.device
     out = torch.empty((ops.b, ops.s, ops.h, ops.d), dtype=out_dtype, device=dev)
     p = _attn_params(ops, cfg, sm_scale)
-    stats = row_skips = None
+    stats = row_skips = wave_tiles = None
     if cfg.blasst_lambda is not None:
         if return_blasst_stats:
             nblk = (ops.s + cfg.p_requant_block_m - 1) // cfg.p_requant_block_m
@@ -198,6 +214,10 @@ def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, retur
         if return_row_skips:
             row_skips = torch.zeros((ops.b * ops.h, ops.s), dtype=torch.float32, device=dev)
             p.blasst_row_skips = row_skips.data_ptr()
+        if return_wave_tiles:
+            nw = (ops.s + 127) // 128 * 4
+            wave_tiles = torch.zeros((ops.b * ops.h, nw, 2), dtype=torch.int32, device=dev)
+            p.blasst_wave_tiles = wave_tiles.data_ptr()
     p.out = out.data_ptr()
     p.out_dtype = _lib.DTYPE_CODE[out_dtype]
     _lib.check(lib.lbfq_attention_fwd(p, _lib.stream_handle(dev)), "lbfq_attention_fwd")
@@ -206,6 +226,8 @@ def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, retur
         res.append(stats)
     if return_row_skips:
         res.append(row_skips)
+    if return_wave_tiles:
+        res.append(wave_tiles)
     return res[0] if len(res) == 1 else tuple(res)
 
 

@@ -175,3 +175,16 @@ def check_assembly(s_path: str) -> list:
 def check_object(obj: str) -> list:
     asm = disassemble(obj)
     return scale_dst_overlaps(asm) + m0_lds_dma_hazards(asm)
+
+
+def scratch_kernels(s_text: str, name_part: str = "attn_fwd_kernel") -> list:
+    """Kernels (whose symbol contains ``name_part``) that spill registers:
+    [(symbol, scratch loads and stores in the body)] from a device assembly
+    file.  (A reserved private segment that no instruction touches is not
+    counted.)"""
+    out = []
+    for m in re.finditer(r"^(\S*" + re.escape(name_part) + r"\S*):[^\n]*\n(.*?)^\.Lfunc_end", s_text, re.M | re.S):
+        n = len(re.findall(r"^\s*scratch_(?:load|store)\w*\s", m.group(2), re.M))
+        if n:
+            out.append((m.group(1), n))
+    return out

@@ -8,8 +8,8 @@ follow an SALU write of M0 (GFX9-family parts need one wait state between
 them; inline asm hides the pair from the compiler's hazard recognizer).  No
 inline asm may touch an MFMA's destination or SrcC registers inside the
 hazard window (gfx950 does not interlock XDL results; the compiler only
-protects its own instructions).  Runs
-on the objects the last build left in ``_build``; skipped when there is no
+protects its own instructions).  No attention kernel spills registers to
+scratch memory.  Runs on the objects the last build left in ``_build``; skipped when there is no
 build.
 """
 
@@ -79,3 +79,26 @@ def test_no_inline_asm_inside_mfma_hazard_window(obj):
     if not os.path.exists(s_path):
         pytest.skip("no device assembly (built without -save-temps)")
     assert mfma_check.check_assembly(s_path) == []
+
+
+def test_parser_finds_scratch_kernels():
+    text = ("_ZN9lbfq_attn15attn_fwd_kernelILi128EEEvNS_5KArgsE: ; @x\n"
+            "\tv_mov_b32 v0, 0\n\tscratch_store_dword off, v2, off offset:28 ; 4-byte Folded Spill\n"
+            "\tscratch_load_dword v2, off, off offset:28 ; 4-byte Folded Reload\n.Lfunc_end0:\n"
+            "_ZN9lbfq_attn15attn_fwd_kernelILi64EEEvNS_5KArgsE:\n\tv_mov_b32 v0, 0\n.Lfunc_end1:\n"
+            "_ZN4lbfq11other_kernelEv:\n\tscratch_store_dword off, v2, off\n.Lfunc_end2:\n")
+    assert mfma_check.scratch_kernels(text) == [("_ZN9lbfq_attn15attn_fwd_kernelILi128EEEvNS_5KArgsE", 2)]
+
+
+ATTN_OBJS = [o for o in OBJS if os.path.basename(o).startswith("lbfq_attn")]
+
+
+@pytest.mark.parametrize("obj", ATTN_OBJS, ids=[os.path.basename(o) for o in ATTN_OBJS])
+def test_attention_kernels_do_not_spill(obj):
+    import build_lib
+    s_path = build_lib.device_asm(obj)
+    if not os.path.exists(s_path):
+        pytest.skip("no device assembly (built without -save-temps)")
+    with open(s_path) as f:
+        assert mfma_check.scratch_kernels(f.read()) == []
+

@@ -189,13 +189,23 @@ def test_blasst_row_skips_bit_exact(gpu, name):
     cfg = _cfg(blasst_lambda=0.05, **SKIP_CASES[name])
     q, k, v = _inputs(n=1024, seed=zlib.crc32(name.encode()) % 1000, field=(4, 16, 16))
     ops, sm = parity.kernel_operands(q, k, v, cfg, gpu)
-    out, rsk = launch_attention(ops, cfg, sm, torch.bfloat16, return_row_skips=True)
+    out, rsk, wt = launch_attention(ops, cfg, sm, torch.bfloat16, return_row_skips=True, return_wave_tiles=True)
     u = parity.kernel_scores(ops, cfg, sm)
     rep, dbg_rep = parity.replay(q, k, v, cfg, ops, u)
     order = dbg_rep["order"]
     rs_rep = parity.unpermute_rows(dbg_rep["row_skips"].reshape(ops.b * ops.h, ops.s), order)
     assert torch.equal(rsk.cpu(), rs_rep)
     assert rs_rep.sum() > 0, "test input should make BLASST skip"
+    # per wave of 32 kernel rows: tiles that all / some of its rows skipped
+    sk = torch.stack(dbg_rep["skip"], -1).reshape(ops.b * ops.h, ops.s, -1)
+    nw = wt.shape[1]
+    skw = torch.zeros(ops.b * ops.h, nw * 32, sk.shape[-1], dtype=torch.bool)
+    skw[:, :ops.s] = sk
+    skw = skw.view(ops.b * ops.h, nw, 32, -1)
+    assert torch.equal(wt[..., 0].cpu(), skw.all(2).sum(-1).int())
+    assert torch.equal(wt[..., 1].cpu(), skw.any(2).sum(-1).int())
+    print(f"{name}: wave tiles all-skip {int(wt[..., 0].sum())}, some-skip {int(wt[..., 1].sum())}, "
+          f"of {nw * ops.b * ops.h * sk.shape[-1]}")
     parity.strict_check(out.cpu(), rep, name, allowance=dbg_rep["flip_allowance_nhd"])
     ref, dbg_ref = opipe.fake_quant_attention(q, k, v, cfg, return_debug=True)
     compared, near, disagree = parity.skip_agreement(rsk, dbg_ref, u, order)
@@ -368,3 +378,62 @@ def test_full_length_padded_wan_shapes(gpu, config):
         print(f"config {config}: skip rate of the sample {got_skips.sum() / (got_skips.numel() * ops.s / 64):.3f}")
     else:
         assert c_ref >= COS_MIN
+
+
+@pytest.mark.parametrize("v_kind", [0, 2])
+def test_v_tile_colsum_matches_decoded_sums(gpu, v_kind):
+    """lbfq_v_tile_colsum: per 64-key tile, the column sums of the decoded V^T
+    codes (MX: times 2^(e-127) of the key block), against a float64 sum of the
+    oracle's E4M3 decode, within fp32 summation error; S ragged (partial last
+    tile sums only its valid keys)."""
+    import numpy as np
+
+    from low_bit_fake_quant.attention_kernel import v_tile_colsum
+    from oracle import fp8
+    g = torch.Generator().manual_seed(5 + v_kind)
+    b, h, d, P, s = 1, 3, 128, 384, 320 if v_kind == 2 else 300
+    codes = torch.randint(0, 256, (b, h, d, P), generator=g, dtype=torch.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # no NaN codes (the quantisers never write them)
+    vb = 64
+    ve = torch.randint(120, 135, (b, h, s // vb, d), generator=g, dtype=torch.uint8)
+    out = v_tile_colsum(codes.to(gpu), ve.to(gpu), v_kind, vb, s).cpu().double()
+    val = torch.from_numpy(fp8.decode(codes.numpy()).astype(np.float64))  # (b,h,d,P)
+    nt = (s + 63) // 64
+    for t in range(nt):
+        k0, k1 = 64 * t, min(64 * t + 64, s)
+        want = val[..., k0:k1].sum(-1)                       # (b,h,d)
+        mag = val[..., k0:k1].abs().sum(-1)
+        if v_kind == 2:
+            sc = torch.pow(2.0, ve[:, :, k0 // vb, :].double() - 127)
+            want, mag = want * sc, mag * sc
+        got = out.view(b, h, -1, d)[:, :, t]
+        assert ((got - want).abs() <= mag * 2.0 ** -21 + 1e-30).all(), t
+
+
+def test_blasst_elided_tiles_match_the_mfma_path(gpu):
+    """Tiles that every row of a wave skips are applied as fill x V column
+    sums (no softmax, no rescale, zero P codes for the next PV).  With and
+    without the column-sum table (every tile through the PV MFMAs) the output
+    meets the strict bound against the reference algorithm replayed on the
+    kernel's scores, and some tiles were elided.  (The two differ by fp32
+    reassociation and by the FP8 MFMA's accumulation error, which the fp32
+    column sums do not have.)"""
+    from low_bit_fake_quant.attention_kernel import launch_attention
+    for fill, p_quant in (("mean_a1.5", "dynamic"), ("max", "elementwise"), ("thr_a0.25", "mx")):
+        cfg = _cfg(qk_quant="fp8_block", fp8_block_size=64, smoothing="full", q_smooth_block_size=256,
+                   q_kmeans_k=16, p_quant=p_quant, p_mx_block_n=64,
+                   rowmax_mode="qm_k" if p_quant == "dynamic" else "online", blasst_lambda=0.05, blasst_fill=fill)
+        q, k, v = _inputs(n=1024, seed=21, field=(4, 16, 16))
+        ops, sm = parity.kernel_operands(q, k, v, cfg, gpu)
+        assert ops.v_colsum is not None
+        out, wt = launch_attention(ops, cfg, sm, torch.bfloat16, return_wave_tiles=True)
+        ref = launch_attention(dataclasses.replace(ops, v_colsum=None), cfg, sm, torch.bfloat16)
+        assert wt[..., 0].sum() > 0, "test input should make whole waves skip"
+        u = parity.kernel_scores(ops, cfg, sm)
+        rep, dbg = parity.replay(q, k, v, cfg, ops, u)
+        alw = dbg["flip_allowance_nhd"]
+        parity.strict_check(out.cpu(), rep, f"elided-{fill}", allowance=alw)
+        parity.strict_check(ref.cpu(), rep, f"mfma-{fill}", allowance=alw)
+        d = (out.float() - ref.float()).abs()
+        print(f"{fill}/{p_quant}: elided wave tiles {int(wt[..., 0].sum())}, elided vs MFMA path max|diff| "
+              f"{d.max().item():.3e}, {int((d > 0).sum())} of {d.numel()} outputs differ")
