@@ -192,6 +192,12 @@ typedef struct {
                                   /* and no V smoothing, a full tile that all 32    */
                                   /* rows of a wave skip is applied as fill x these */
                                   /* sums instead of its PV MFMAs                   */
+  int block_n;                    /* keys per row-max update, P scale and BLASST   */
+                                  /* decision (the reference's block_n): 64 or 128 */
+                                  /* (0 = 64)                                      */
+  const float* rowmax_init;       /* (B,H,S) fp32 initial row max in log2 units     */
+                                  /* (rowmax_init_bhs * log2(e)), rows in kernel    */
+                                  /* order, or NULL; not with rowmax_est            */
 } lbfq_attn_params;
 
 int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t stream);

@@ -43,6 +43,9 @@ UNITS = {
     "lbfq_attn_p0.hip": ATTN_FLAGS,
     "lbfq_attn_p1.hip": ATTN_FLAGS,
     "lbfq_attn_p2.hip": ATTN_FLAGS,
+    "lbfq_attn_b128_p0.hip": ATTN_FLAGS,
+    "lbfq_attn_b128_p1.hip": ATTN_FLAGS,
+    "lbfq_attn_b128_p2.hip": ATTN_FLAGS,
 }
 
 
@@ -79,7 +82,7 @@ def _check_mfma(objs: list[str]) -> None:
         if os.path.exists(s_path):
             with open(s_path) as f:
                 for sym, nb in mfma_check.scratch_kernels(f.read()):
-                    print(f"warning: {sym} spills {nb} bytes to scratch", file=sys.stderr)
+                    print(f"warning: {sym} spills registers ({nb} scratch loads / stores)", file=sys.stderr)
     if bad:
         lines = "\n".join(f"{os.path.basename(o)}: {x}" for o, b in bad.items() for x in b[:4])
         raise RuntimeError("gfx950 code check failed (a scaled MFMA reading a scale from its own destination "
@@ -95,7 +98,7 @@ def device_asm(obj: str) -> str:
 
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=len(UNITS)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(len(UNITS), os.cpu_count() or 8)) as ex:
         objs = list(ex.map(lambda kv: _compile(*kv), UNITS.items()))
     _check_mfma(objs)
     tmp = OUT + ".tmp"

@@ -70,6 +70,9 @@ int make_kargs(const lbfq_attn_params* p, KArgs& a, const char* who) {
   LBFQ_CHECK_ARG(p->qk_mx || (p->qk_block >= 16 && is_pow2(p->qk_block)),
                  "%s: fp8_block size must be a power of two >= 16; got %d", who, p->qk_block);
   LBFQ_CHECK_ARG(!p->rowmax_est || p->qk_bias, "%s: rowmax_est needs the qm correction table", who);
+  LBFQ_CHECK_ARG(!(p->rowmax_est && p->rowmax_init), "%s: rowmax_init and rowmax_est are mutually exclusive", who);
+  LBFQ_CHECK_ARG(p->block_n == 0 || p->block_n == 64 || p->block_n == 128, "%s: block_n must be 64 or 128; got %d",
+                 who, p->block_n);
   LBFQ_CHECK_ARG(!p->qk_bias || (p->q_group >= 32 && is_pow2(p->q_group) && p->S % p->q_group == 0),
                  "%s: q_group must be a power of two >= 32 dividing S", who);
   const bool blasst = p->blasst_lambda > 0.0f;
@@ -110,6 +113,7 @@ int make_kargs(const lbfq_attn_params* p, KArgs& a, const char* who) {
   a.row_skips = p->blasst_row_skips;
   a.wave_tiles = p->blasst_wave_tiles;
   a.vcol = p->v_tile_colsum;
+  a.rowmax_init = p->rowmax_init;
   a.out = p->out;
   a.out_dtype = p->out_dtype;
   a.out_row_map = p->out_row_map;
@@ -248,17 +252,20 @@ extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t strea
   if (make_kargs(p, a, "lbfq_attention_fwd")) return -1;
   LBFQ_CHECK_ARG(p->v_codes_t && p->out, "lbfq_attention_fwd: missing tensor");
   LBFQ_CHECK_ARG(p->v_kind >= 0 && p->v_kind <= 2 && p->v_scale, "lbfq_attention_fwd: bad V kind");
+  const int bn = p->block_n == 128 ? 128 : kTN;
   LBFQ_CHECK_ARG(p->v_kind == 0 || (p->v_block >= kTN && is_pow2(p->v_block) && p->S % p->v_block == 0),
                  "lbfq_attention_fwd: V block (%d) must be a power of two >= %d dividing S", p->v_block, kTN);
+  LBFQ_CHECK_ARG(p->v_kind != 1 || p->v_block % bn == 0,
+                 "lbfq_attention_fwd: v_block_size (%d) must be a multiple of block_n (%d)", p->v_block, bn);
   LBFQ_CHECK_ARG(p->p_mode >= 0 && p->p_mode <= 2, "lbfq_attention_fwd: bad P mode");
-  LBFQ_CHECK_ARG(!p->v_alpha || (p->v_smooth_block >= kTN && is_pow2(p->v_smooth_block) &&
+  LBFQ_CHECK_ARG(!p->v_alpha || (p->v_smooth_block >= bn && is_pow2(p->v_smooth_block) &&
                                   p->S % p->v_smooth_block == 0),
-                 "lbfq_attention_fwd: v_smooth_block must be a power of two >= %d dividing S", kTN);
+                 "lbfq_attention_fwd: v_smooth_block must be a power of two >= block_n (%d) dividing S", bn);
   LBFQ_CHECK_ARG(!p->blasst_stats || p->block_m > 0, "lbfq_attention_fwd: block_m must be positive");
   LBFQ_CHECK_ARG(p->blasst_lambda < 1.0f, "lbfq_attention_fwd: lambda must be < 1");
   LBFQ_CHECK_ARG(p->blasst_lambda <= 0.0f || p->blasst_fill != FILL_UTA ||
-                     (p->blasst_uta_bins > 0 && kTN % p->blasst_uta_bins == 0),
-                 "lbfq_attention_fwd: UTA bins must divide %d", kTN);
+                     (p->blasst_uta_bins > 0 && bn % p->blasst_uta_bins == 0),
+                 "lbfq_attention_fwd: UTA bins must divide block_n (%d)", bn);
   LBFQ_CHECK_ARG(p->blasst_fill >= FILL_ZERO && p->blasst_fill <= FILL_UTA, "lbfq_attention_fwd: bad fill kind");
   LBFQ_CHECK_ARG(p->out_dtype >= 0 && p->out_dtype <= 2, "lbfq_attention_fwd: bad out dtype");
 
@@ -269,6 +276,11 @@ extern "C" int lbfq_attention_fwd(const lbfq_attn_params* p, lbfq_stream_t strea
   const int D = static_cast<int>(p->D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int bl = !blasst ? 0 : p->blasst_fill != FILL_UTA ? 1 : (p->blasst_uta_bins <= 16 ? 2 : 3);
+  if (bn == 128) {
+    if (p->p_mode == 0) return launch_b128_p0(a, D, mx, rb, bl, valpha, st);
+    if (p->p_mode == 1) return launch_b128_p1(a, D, mx, rb, bl, valpha, st);
+    return launch_b128_p2(a, D, mx, rb, bl, valpha, st);
+  }
   if (p->p_mode == 0) return launch_p0(a, D, mx, rb, bl, valpha, st);
   if (p->p_mode == 1) return launch_p1(a, D, mx, rb, bl, valpha, st);
   return launch_p2(a, D, mx, rb, bl, valpha, st);

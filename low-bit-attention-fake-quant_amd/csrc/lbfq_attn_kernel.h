@@ -100,6 +100,7 @@ struct KArgs {
   float* row_skips;
   int* wave_tiles;
   const float* vcol;  // (B*H, P/64, D) V tile column sums, or null
+  const float* rowmax_init;  // (B*H, S) initial row max, log2 units (kernel row order), or null
   void* out;
   int out_dtype;
   const int32_t* out_row_map;
@@ -527,17 +528,157 @@ __device__ __forceinline__ float blasst_fill(const KArgs& a, const float (&u)[32
   return f;
 }
 
+
+// ---- BLASST fills over a 128-key block (block_n = 128) ----------------------
+// The lane holds 64 keys of the row in four 16-key groups: group k = 2 tt + t
+// (tile tt of the block, 32-key half t), keys key0 + 64 tt + 32 t + 16 g + r.
+// Same formulas as the 64-key fills; sample8 takes the keys with
+// rel % 16 == 0 (r == 0; BLOCK_N / 8 = 16, attention_triton.py:270-276).
+template <int P_MODE, bool MASKED>
+__device__ __forceinline__ float blasst_row_fill128(const KArgs& a, const v16f (&s4)[4], const float (&C4)[4],
+                                                    float m_new, float bmax, float off, int key0) {
+  const int fk = a.fill_kind;
+  const float fa = a.fill_alpha;
+  const int nv = MASKED ? (a.S - key0 < 128 ? a.S - key0 : 128) : 128;
+  const float n = static_cast<float>(nv), rn = MASKED ? 1.0f / n : 1.0f / 128.0f;
+  const float max_bound = n * fast_exp2(bmax - m_new + off);
+  float f = 0.0f;  // FILL_ZERO
+  if (fk == FILL_MAX) {
+    f = max_bound * fa * rn;
+  } else if (fk == FILL_MEAN || fk == FILL_LOGN) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (MASKED) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += valid_or(s4[k][r] * C4[k], 0.0f);
+      } else {
+        float p8[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) p8[r] = s4[k][r] + s4[k][r + 8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p8[r] += p8[r + 4];
+        s = fmaf((p8[0] + p8[2]) + (p8[1] + p8[3]), C4[k], s);
+      }
+    }
+    const float mean = xor32_add(s) * rn;  // log2 units
+    if (fk == FILL_MEAN) {
+      f = fminf(fa * n * fast_exp2(mean - m_new + off), max_bound) * rn;
+    } else {
+      float vs = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float c = fmaf(s4[k][r], C4[k], -mean);
+          if constexpr (MASKED) c = valid_or(c, 0.0f);
+          vs = fmaf(c, c, vs);
+        }
+      const float var2 = xor32_add(vs) * rn;  // log2 units squared
+      f = fminf(n * fast_exp2(mean + 0.5f * var2 * kLn2 - m_new + off), max_bound) * rn;
+    }
+  } else if (fk == FILL_SAMPLE8) {
+    const float c0 = off - m_new;
+    float sp = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sp += fast_exp2(s4[k][0] * C4[k] + c0);
+    sp = xor32_add(sp);
+    const float cnt = static_cast<float>((nv + 15) / 16);
+    f = fminf(fa * n * sp / cnt, max_bound) * rn;
+  } else if (fk == FILL_THR) {
+    const float offs = P_MODE == 0 ? exp2f(static_cast<float>(a.p_max_offset)) : 1.0f;
+    f = fa * n * a.lam * offs * rn;
+  }
+  return f;
+}
+
+// UTA over a 128-key block, bins of BS = 128 / bins keys: the fill of each
+// run of min(BS, 16) lane keys (runs of a bin that spans groups or both lanes
+// of the row share the bin's statistics) into fr[0 .. 64 / RUN); returns the
+// row's largest fill.
+template <int BS, bool MASKED>
+__device__ __forceinline__ float uta128_runs(const v16f (&s4)[4], const float (&C4)[4], float m_new, float off,
+                                             float fa, float (&fr)[64]) {
+  constexpr int RUN = BS < 16 ? BS : 16;
+  constexpr int NR = 64 / RUN;
+  float s[NR], mx[NR], c[NR];
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    const int k = (RUN * j) >> 4, r0 = (RUN * j) & 15;
+    s[j] = 0.0f; mx[j] = -INFINITY; c[j] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RUN; ++r) {
+      const float x = s4[k][r0 + r] * C4[k];
+      s[j] += MASKED ? valid_or(x, 0.0f) : x;
+      mx[j] = hmax(mx[j], x);
+      c[j] += (!MASKED || x != -INFINITY) ? 1.0f : 0.0f;
+    }
+  }
+  if constexpr (BS >= 64) {  // a bin spans the groups of a tile (64) or of the block (128)
+    constexpr int G = BS / 32;  // lane groups per bin
+#pragma unroll
+    for (int j = 0; j < NR; j += G) {
+#pragma unroll
+      for (int i = 1; i < G; ++i) { s[j] += s[j + i]; mx[j] = hmax(mx[j], mx[j + i]); c[j] += c[j + i]; }
+#pragma unroll
+      for (int i = 1; i < G; ++i) { s[j + i] = s[j]; mx[j + i] = mx[j]; c[j + i] = c[j]; }
+    }
+  }
+  if constexpr (BS >= 32) {  // and both lanes of the row
+#pragma unroll
+    for (int j = 0; j < NR; ++j) { s[j] = xor32_add(s[j]); mx[j] = xor32_max(mx[j]); c[j] = xor32_add(c[j]); }
+  }
+  float fmx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    const float sc_b = fmaxf(c[j], 1.0f), rc = __builtin_amdgcn_rcpf(sc_b);
+    const float f = fminf(fa * sc_b * fast_exp2(s[j] * rc - m_new + off), sc_b * fast_exp2(mx[j] - m_new + off)) * rc;
+    fmx = fmaxf(fmx, f);
+    fr[j] = f;
+  }
+  return xor32_max(fmx);
+}
+
+// The lane's UTA fill codes of both tiles (fpk[8 tt + q]: keys 4q..4q+3 of
+// tile tt, in the order of the P codes) and the sum of its pre-quant fills.
+template <int BS, int P_MODE>
+__device__ __forceinline__ void uta128_pack(const v16f (&s4)[4], const float (&fr)[64], float qmul_f,
+                                            uint32_t (&fpk)[16], float& fsum) {
+  constexpr int RUN = BS < 16 ? BS : 16;
+  float sum = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int jl = 4 * w + i;  // lane key 32 tt + 16 t + r
+      const float f = s4[jl >> 4][jl & 15] != -INFINITY ? fr[jl / RUN] : 0.0f;
+      sum += P_MODE == 0 ? f : f * qmul_f;
+      v[i] = P_MODE == 0 ? fminf(f, kFp8Max) : f * qmul_f;
+    }
+    const int wd = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], __float_as_int(v[0]), false);
+    fpk[w] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], wd, true));
+  }
+  fsum = sum;
+}
+
 // BL: BLASST off (0); with a fill of one value per row and tile (1); with the
 // UTA fill of at most 16 bins (2: packed fill codes per lane); with the UTA
 // fill of 32 or 64 bins (3: one fill code per key in 32 registers, one wave
 // per SIMD).  BLASST together with V smoothing also runs one wave per SIMD.
-template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA>
-__global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1 : 2) attn_fwd_kernel(const KArgs a) {
+// BN: the reference's block_n, the keys that share one row-max update, one
+// P scale and one BLASST decision: 64 (one MFMA tile per step) or 128 (two).
+constexpr int attn_waves_per_simd(int bl, bool valpha, int bn) {
+  return (bl == 3 || (bl != 0 && valpha) || (bn == 128 && bl != 0)) ? 1 : 2;
+}
+template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA, int BN>
+__global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN)) attn_fwd_kernel(const KArgs a) {
+  static_assert(BN == 64 || BN == 128, "block_n is 64 or 128");
   constexpr bool BLASST = BL != 0;
   // BLASST with one fill value per row and tile, without V smoothing: a tile
   // that every row of the wave skips adds fill * (column sums of V) to the
   // accumulator instead of running its four PV MFMAs
-  constexpr bool ELIDE = BL == 1 && !VALPHA;
+  constexpr bool ELIDE = BL == 1 && !VALPHA && BN == 64;
   using VM = VMeta<D, ELIDE>;
   constexpr int NH = D / 64;          // 64-wide contraction halves of D
   constexpr int NDB = D / 32;         // 32-row blocks of O^T
@@ -615,6 +756,10 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   }
   float m2 = -INFINITY;  // running row max, log2 units
   if constexpr (HAS_EST) m2 = a.rowmax[bh * a.G + grp];
+  // rowmax_init (attention_triton.py:127-130): the online max starts at the given value
+  if constexpr (!HAS_EST) {
+    if (a.rowmax_init && qvalid) m2 = a.rowmax_init[static_cast<size_t>(bh) * S + qi];
+  }
   const float est2 = m2;
   const bool dyn_est = HAS_EST && !BLASST && P_MODE == 2 && a.rowmax_dynamic;
   const float off = P_MODE == 0 ? static_cast<float>(a.p_max_offset) : 0.0f;
@@ -826,6 +971,8 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     acc[db] = mfma32<true>(va, pcodes, acc[db], ve, pe_);
   };
 
+  int ndec = nt;  // row-max / BLASST decisions per row
+  if constexpr (BN == 64) {
   // prologue: tiles 0 and 1 complete, K codes of tile 2.  V slot 3 stands for
   // tile -1: zero codes with unit scales, so the PV that the first step issues
   // for the previous tile adds exactly zero.
@@ -1266,6 +1413,245 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
         }
     }
   }
+  } else {
+    // ---- block_n = 128 (attention_triton.py:109-407 with BLOCK_N = 128) -------------
+    // One step per 128-key block b: the scores of its two 64-key tiles (ring
+    // slots 2b % 4 and (2b + 1) % 4), one row-max update, BLASST decision, fill
+    // and P scale over the 128 keys, the P codes of both tiles, then the
+    // accumulator rescale and the PV of both tiles.  The K/V tiles of block
+    // b + 1 are copied into the other two slots during the step, which ends
+    // with all copies landed and a barrier.
+    const int nb = (S + 127) / 128;
+    ndec = nb;
+    auto load_block = [&](int bb) {
+      const int t0 = 2 * bb, t1 = 2 * bb + 1;
+      const int c0 = t0 < nt ? t0 : nt - 1, c1 = t1 < nt ? t1 : nt - 1;
+      load_k(c0, t0 & 3);
+      load_k(c1, t1 & 3);
+      load_v(c0, t0 & 3);
+      load_v(c1, t1 & 3);
+    };
+    load_block(0);
+    lds_publish<0>();
+    auto step128 = [&](const int bb, auto masked_tag) __attribute__((always_inline)) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      const int key0 = bb * 128;
+      const int slA = (2 * bb) & 3, slB = (2 * bb + 1) & 3;
+      if (bb + 1 < nb) load_block(bb + 1);
+      // scores of both tiles: s4[2 tt + t] for tile tt, C4 its score scales
+      v16f s4[4];
+      float C4[4];
+      auto qk_tile = [&](int sl, int o) __attribute__((always_inline)) {
+        const BiasIn x = bias_fetch(sl);
+        C4[o] = Ct_next[0];
+        C4[o + 1] = Ct_next[1];
+        bias_store(x);
+        qk_init(s4[o], 0);
+        qk_init(s4[o + 1], 1);
+        pin(s4[o]);  // never a known constant at the MFMA (see acc)
+        pin(s4[o + 1]);
+#pragma unroll
+        for (int i = 0; i < NQK; ++i) s4[o + i / NH] = qk_mfma(i, qk_read(sl, i), s4[o + i / NH], qk_scale(sl, i));
+      };
+      qk_tile(slA, 0);
+      qk_tile(slB, 2);
+      if constexpr (MASKED) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (key0 + 64 * (k >> 1) + 32 * (k & 1) + 16 * g + r >= S) s4[k][r] = -INFINITY;
+      }
+      float bmax;
+      {
+        float mk[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float m = hmax3(s4[k][0], s4[k][1], s4[k][2]);
+#pragma unroll
+          for (int r = 3; r < 15; r += 2) m = hmax3(m, s4[k][r], s4[k][r + 1]);
+          mk[k] = hmax(m, s4[k][15]) * C4[k];  // C > 0
+        }
+        bmax = xor32_max(hmax(hmax(mk[0], mk[1]), hmax(mk[2], mk[3])));
+      }
+      // row max, BLASST decision (as the 64-key step, over 128 keys)
+      float alpha, m_new;
+      int pe = 127;
+      float sig_p = 1.0f;
+      bool skip = false;
+      if constexpr (BLASST) {
+        const float mij = hmax(m2, bmax);
+        skip = qvalid && (bmax - mij) < a.log2_lam;
+        alpha = skip ? 1.0f : fast_exp2(m2 - mij);
+        m_new = skip ? m2 : mij;
+        skipped += skip ? 1.0f : 0.0f;
+      } else if constexpr (HAS_EST && P_MODE == 2) {
+        const bool lzero = bb == 0;
+        const float ms = hmax(max_seen, bmax);
+        const bool under = (bmax - m2) > 16.0f;
+        const bool over = (m2 - ms) > 32.0f;
+        const float down = lzero ? ms : fmaxf(ms + 32.0f, m2 - 80.0f * kLog2e);
+        const bool adjust = dyn_est && (under || over);
+        m_new = adjust ? (under ? bmax : down) : m2;
+        alpha = adjust ? (lzero ? 0.0f : fast_exp2(m2 - m_new)) : 1.0f;
+        max_seen = dyn_est ? ms : max_seen;
+      } else if constexpr (HAS_EST) {
+        m_new = est2;
+        alpha = 1.0f;
+      } else {
+        m_new = hmax(m2, bmax);
+        alpha = fast_exp2(m2 - m_new);
+      }
+      float fmax = 0.0f;
+      bool any_skip = false;
+      float fr[BL == 2 ? 64 : 1];
+      if constexpr (BLASST) {
+        any_skip = __any(skip);
+        if (any_skip) {
+          if constexpr (BL == 1) {
+            fmax = blasst_row_fill128<P_MODE, MASKED>(a, s4, C4, m_new, bmax, off, key0);
+          } else {
+            switch (128 / a.uta_bins) {
+              case 1: fmax = uta128_runs<1, MASKED>(s4, C4, m_new, off, a.fill_alpha, fr); break;
+              case 2: fmax = uta128_runs<2, MASKED>(s4, C4, m_new, off, a.fill_alpha, fr); break;
+              case 4: fmax = uta128_runs<4, MASKED>(s4, C4, m_new, off, a.fill_alpha, fr); break;
+              case 8: fmax = uta128_runs<8, MASKED>(s4, C4, m_new, off, a.fill_alpha, fr); break;
+              case 16: fmax = uta128_runs<16, MASKED>(s4, C4, m_new, off, a.fill_alpha, fr); break;
+              case 32: fmax = uta128_runs<32, MASKED>(s4, C4, m_new, off, a.fill_alpha, fr); break;
+              case 64: fmax = uta128_runs<64, MASKED>(s4, C4, m_new, off, a.fill_alpha, fr); break;
+              default: fmax = uta128_runs<128, MASKED>(s4, C4, m_new, off, a.fill_alpha, fr); break;
+            }
+          }
+        }
+      }
+      // P scale of the row over the block (attention_triton.py:330-370)
+      float T, s_lp, qmul_f = 1.0f;
+      if constexpr (P_MODE == 0) {
+        T = m_new - off;
+        s_lp = 1.0f;
+      } else if constexpr (P_MODE == 1) {
+        const float ra = fmaxf(skip ? fmax : fast_exp2(bmax - m_new), kAmaxFloor);
+        int e = ceil_log2_div448(ra);
+        e = e < -127 ? -127 : (e > 127 ? 127 : e);
+        T = m_new + static_cast<float>(e);
+        s_lp = __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+        qmul_f = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+        pe = e + 127;
+      } else {
+        const float ra = skip ? fmax : fast_exp2(bmax - m_new);
+        const bool floored = !(ra > 1e-12f);
+        const float rf = floored ? 1e-12f : ra;
+        s_lp = rf * (1.0f / kFp8Max);
+        T = (floored ? m_new + kLog2DynFloor : bmax) - kLog2Fp8Max;
+        sig_p = s_lp;
+        if constexpr (BLASST) qmul_f = kFp8Max * __builtin_amdgcn_rcpf(rf);
+      }
+      float fq = 0.0f;
+      int fqw = 0;
+      uint32_t fpk[BL == 2 ? 16 : 1];
+      float fsum = 0.0f;
+      if constexpr (BL == 1) {
+        fq = P_MODE == 0 ? fminf(fmax, kFp8Max) : fmax * qmul_f;
+        fqw = __builtin_amdgcn_cvt_pk_fp8_f32(fq, fq, __float_as_int(fq), false);
+        fqw = __builtin_amdgcn_cvt_pk_fp8_f32(fq, fq, fqw, true);
+      } else if constexpr (BL == 2) {
+#pragma unroll
+        for (int w = 0; w < 16; ++w) fpk[w] = 0u;
+        if (any_skip) {
+          switch (128 / a.uta_bins) {
+            case 1: uta128_pack<1, P_MODE>(s4, fr, qmul_f, fpk, fsum); break;
+            case 2: uta128_pack<2, P_MODE>(s4, fr, qmul_f, fpk, fsum); break;
+            case 4: uta128_pack<4, P_MODE>(s4, fr, qmul_f, fpk, fsum); break;
+            case 8: uta128_pack<8, P_MODE>(s4, fr, qmul_f, fpk, fsum); break;
+            case 16: uta128_pack<16, P_MODE>(s4, fr, qmul_f, fpk, fsum); break;
+            case 32: uta128_pack<32, P_MODE>(s4, fr, qmul_f, fpk, fsum); break;
+            case 64: uta128_pack<64, P_MODE>(s4, fr, qmul_f, fpk, fsum); break;
+            default: uta128_pack<128, P_MODE>(s4, fr, qmul_f, fpk, fsum); break;
+          }
+        }
+      }
+      (void)fq;
+      (void)fqw;
+      if constexpr (BLASST) {
+        wt_all += __all(skip) ? 1 : 0;
+        wt_any += any_skip ? 1 : 0;
+      }
+      // P codes of both tiles (keys 32 t + 16 g + r of tile tt in word 8 tt + 2 (2 t + r / 8) ...)
+      const bool clamp = P_MODE == 0 && (HAS_EST || a.p_max_offset > 8);
+      v8i popt[2];
+      float ps4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          float pq[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int jl = 32 * tt + 4 * q + i, k = jl >> 4, r = jl & 15;
+            pq[i] = fast_exp2(fmaf(s4[k][r], C4[k], -T));
+            if constexpr (BL == 1) pq[i] = skip ? (s4[k][r] == -INFINITY ? 0.0f : fq) : pq[i];
+            ps4[i] += pq[i];
+            if constexpr (P_MODE == 0) pq[i] = clamp ? fminf(pq[i], kFp8Max) : pq[i];
+          }
+          const int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pq[0], pq[1], __float_as_int(pq[0]), false);
+          int word = __builtin_amdgcn_cvt_pk_fp8_f32(pq[2], pq[3], wd, true);
+          if constexpr (BL == 2) word = skip ? static_cast<int>(fpk[8 * tt + q]) : word;
+          popt[tt][q] = word;
+        }
+      float psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+      if constexpr (BL == 1) {
+        // a skipped row sums its pre-quant fill once per valid key of the lane
+        float nvl = 64.0f;
+        if constexpr (MASKED) {
+          int c = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) c += min(max(S - key0 - 64 * (k >> 1) - 32 * (k & 1) - 16 * g, 0), 16);
+          nvl = static_cast<float>(c);
+        }
+        psum = skip ? (P_MODE == 0 ? fmax : fmax * qmul_f) * nvl : psum;
+      }
+      if constexpr (BL == 2) psum = skip ? fsum : psum;
+      psum *= s_lp;
+      l = l * alpha + psum;
+      // accumulator rescale (alpha, dynamic P scale, fp8_block V scale), then
+      // the PV of both tiles in the new units
+      const float vsc = vmeta[slA].vsc[0];
+      float sig_new = sig_p;
+      sig_new *= v_blk ? vsc : 1.0f;
+      const float rsig = __builtin_amdgcn_rcpf(sig_new);
+      const float f = alpha * sigma * rsig;
+      sigma = sig_new;
+      if (P_MODE == 2 || __any(f != 1.0f)) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[db][r] *= f;
+      }
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        pv_mfma(db, pv_read(slA, db), popt[0], pe, pv_scale(slA, db));
+        pv_mfma(db, pv_read(slB, db), popt[1], pe, pv_scale(slB, db));
+      }
+      if constexpr (VALPHA) {  // rowsum(P_deq) / sigma (x) alpha_v of the block (v_smooth_block >= 128)
+        const v16f zero = {};
+        v16f rs = mfma32<false>(ones, popt[0], zero, 0, 0);
+        rs = mfma32<false>(ones, popt[1], rs, 0, 0);
+        const float w = rs[0] * s_lp * rsig;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int d = 32 * db + 8 * (r >> 2) + 4 * g + (r & 3);
+            acc[db][r] = fmaf(w, vmeta[slA].valpha[d], acc[db][r]);
+          }
+      }
+      m2 = m_new;
+      lds_publish<0>();
+    };
+    const int nbfull = (S % 128) ? nb - 1 : nb;
+    for (int bb = 0; bb < nbfull; ++bb) step128(bb, std::false_type{});
+    if (nbfull < nb) step128(nb - 1, std::true_type{});
+  }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
   // ---- epilogue ---------------------------------------------------------------------
@@ -1274,7 +1660,7 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
     if (a.stats && g == 0 && qvalid) {
       const int rb = qi / a.block_m;
       atomicAdd(a.stats + (static_cast<size_t>(rb) * (a.B * a.H) + bh) * 2 + 0, skipped);
-      atomicAdd(a.stats + (static_cast<size_t>(rb) * (a.B * a.H) + bh) * 2 + 1, static_cast<float>(nt));  // tiles seen
+      atomicAdd(a.stats + (static_cast<size_t>(rb) * (a.B * a.H) + bh) * 2 + 1, static_cast<float>(ndec));  // decisions
     }
   }
   if constexpr (BLASST) {
@@ -1322,24 +1708,33 @@ __global__ void __launch_bounds__(kThreads, (BL == 3 || (BL != 0 && VALPHA)) ? 1
   }
 }
 
-// Launch one instantiation (defined in the per-P-mode translation units).
-// bl: 0 no BLASST; BLASST with a per-row fill (1), the UTA fill of <= 16 bins (2)
-// or of 32 / 64 bins (3).
+// Launch one instantiation (defined in the per-P-mode, per-block_n
+// translation units).  bl: 0 no BLASST; BLASST with a per-row fill (1), the
+// UTA fill of <= 16 bins (2) or of 32 / 64 bins (3); with block_n = 128 every
+// UTA fill is bl 2.
 int launch_p0(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
 int launch_p1(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
 int launch_p2(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
+int launch_b128_p0(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
+int launch_b128_p1(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
+int launch_b128_p2(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st);
 
-template <int P_MODE>
+template <int P_MODE, int BN>
 int launch_p(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st) {
   const int nblk = a.B * a.H * a.nqb;
   dim3 grid(static_cast<unsigned>(nblk)), block(kThreads);
 #define LBFQ_L(DD, MX, RBV, BL, VA) \
-  hipLaunchKernelGGL((attn_fwd_kernel<DD, MX, P_MODE, RBV, BL, VA>), grid, block, 0, st, a)
+  hipLaunchKernelGGL((attn_fwd_kernel<DD, MX, P_MODE, RBV, BL, VA, BN>), grid, block, 0, st, a)
 #define LBFQ_VA(DD, MX, RBV, BL) \
   if (valpha) LBFQ_L(DD, MX, RBV, BL, true); else LBFQ_L(DD, MX, RBV, BL, false)
-#define LBFQ_BL(DD, MX, RBV)                                              \
-  if (bl == 3) { LBFQ_VA(DD, MX, RBV, 3); } else if (bl == 2) { LBFQ_VA(DD, MX, RBV, 2); } \
-  else if (bl == 1) { LBFQ_VA(DD, MX, RBV, 1); } else { LBFQ_VA(DD, MX, RBV, 0); }
+#define LBFQ_BL(DD, MX, RBV)                                                                     \
+  if constexpr (BN == 64) {                                                                      \
+    if (bl == 3) { LBFQ_VA(DD, MX, RBV, 3); } else if (bl == 2) { LBFQ_VA(DD, MX, RBV, 2); }     \
+    else if (bl == 1) { LBFQ_VA(DD, MX, RBV, 1); } else { LBFQ_VA(DD, MX, RBV, 0); }             \
+  } else {                                                                                       \
+    if (bl >= 2) { LBFQ_VA(DD, MX, RBV, 2); } else if (bl == 1) { LBFQ_VA(DD, MX, RBV, 1); }     \
+    else { LBFQ_VA(DD, MX, RBV, 0); }                                                           \
+  }
 #define LBFQ_RB(DD, MX)                    \
   if (rb == RB_ONLINE) { LBFQ_BL(DD, MX, RB_ONLINE) }            \
   else if (rb == RB_ONLINE_BIAS) { LBFQ_BL(DD, MX, RB_ONLINE_BIAS) } \

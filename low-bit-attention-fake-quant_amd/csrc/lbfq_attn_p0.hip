@@ -4,6 +4,6 @@
 
 namespace lbfq_attn {
 int launch_p0(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st) {
-  return launch_p<0>(a, D, qk_mx, rb, bl, valpha, st);
+  return launch_p<0, 64>(a, D, qk_mx, rb, bl, valpha, st);
 }
 }  // namespace lbfq_attn

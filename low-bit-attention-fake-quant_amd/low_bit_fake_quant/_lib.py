@@ -83,6 +83,8 @@ class AttnParams(ctypes.Structure):
         ("blasst_row_skips", _vp),
         ("blasst_wave_tiles", _vp),
         ("v_tile_colsum", _vp),
+        ("block_n", _i32),
+        ("rowmax_init", _vp),
     ]
 
 

@@ -315,7 +315,7 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
             # which the per-channel V scales multiply at the end
             v_alpha = v_alpha / v_scale[:, :, None, :]
     v_colsum = None
-    if cfg.blasst_lambda is not None and v_alpha is None:
+    if cfg.blasst_lambda is not None and v_alpha is None and cfg.p_requant_block_n == 64:
         # lets the kernel apply a tile that all rows of a wave skip as fill x column sums
         v_colsum = v_tile_colsum(v_codes, v_scale, v_kind, v_block, s)
     return QuantizedOperands(b=b, s=s, h=h, d=d, P=P, q_codes=q_codes, q_scale=q_scale, k_codes=k_codes,

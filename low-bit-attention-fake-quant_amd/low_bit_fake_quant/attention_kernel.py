@@ -25,6 +25,7 @@ _BLASST_FILL_THR = 5
 _BLASST_FILL_UTA = 6
 
 KERNEL_BLOCK_N = 64   # keys per tile of the gfx950 kernel
+KERNEL_BLOCK_NS = (64, 128)  # block_n values: one or two tiles per row-max / BLASST decision
 
 
 def parse_blasst_fill(mode: str | None, *, alpha: float, uta_bins: int) -> tuple[int, float, int]:
@@ -121,8 +122,8 @@ def validate_kernel_config(cfg, *, s: int, d: int, has_qm: bool, has_v_alpha: bo
     def pow2(x):
         return x > 0 and (x & (x - 1)) == 0
 
-    if block_n != KERNEL_BLOCK_N:
-        raise ValueError(f"the gfx950 P-requant kernel runs p_requant_block_n={KERNEL_BLOCK_N}; got {block_n}")
+    if block_n not in KERNEL_BLOCK_NS:
+        raise ValueError(f"the gfx950 P-requant kernel runs p_requant_block_n in {KERNEL_BLOCK_NS}; got {block_n}")
     if block_m <= 0:
         raise ValueError(f"p_requant_block_m must be > 0; got {block_m}")
     if cfg.qk_quant == "mxfp8" and cfg.mxfp8_block_size != 32:
@@ -178,6 +179,7 @@ def _attn_params(ops, cfg, sm_scale: float) -> "_lib.AttnParams":
         p.blasst_fill, p.blasst_fill_alpha, p.blasst_uta_bins = 0, 1.0, 1
     p.out_row_map = _lib.ptr(ops.out_row_map)
     p.v_tile_colsum = _lib.ptr(getattr(ops, "v_colsum", None))
+    p.block_n = int(cfg.p_requant_block_n)
     return p
 
 
@@ -194,17 +196,27 @@ def v_tile_colsum(v_codes_t: torch.Tensor, v_scale: torch.Tensor, v_kind: int, v
 
 
 def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, return_blasst_stats: bool = False,
-                     return_row_skips: bool = False, return_wave_tiles: bool = False):
+                     return_row_skips: bool = False, return_wave_tiles: bool = False,
+                     rowmax_init: torch.Tensor | None = None):
     """Run the attention kernel on quantised operands; returns NHD output, then
     (when asked) the BLASST stats (ceil(S/block_m), B*H, 2), the per-row
     skipped K-block counts (B*H, S) in output-row order, and per wave of 32
     reordered query rows the number of 64-key tiles that every row of the wave
     skipped (softmax and PV elided) and that some row skipped,
-    (B*H, ceil(S/128)*4, 2) int32."""
+    (B*H, ceil(S/128)*4, 2) int32.  ``rowmax_init`` (B*H, S) fp32: the
+    initial row max of each (reordered) query row in log2 units
+    (attention_triton.py rowmax_init_bhs * log2 e); not with a qm_k estimate."""
     lib = _lib.load()
     dev = ops.q_codes.device
     out = torch.empty((ops.b, ops.s, ops.h, ops.d), dtype=out_dtype, device=dev)
     p = _attn_params(ops, cfg, sm_scale)
+    if rowmax_init is not None:
+        if rowmax_init.shape != (ops.b * ops.h, ops.s) or rowmax_init.dtype != torch.float32 or \
+                rowmax_init.device != dev or not rowmax_init.is_contiguous():
+            raise ValueError(f"rowmax_init must be a contiguous (B*H, S) fp32 tensor on {dev}")
+        if ops.rowmax is not None:
+            raise ValueError("rowmax_init_bhs and rowmax_est_bhs are mutually exclusive")
+        p.rowmax_init = rowmax_init.data_ptr()
     stats = row_skips = wave_tiles = None
     if cfg.blasst_lambda is not None:
         if return_blasst_stats:

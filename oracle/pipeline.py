@@ -114,7 +114,7 @@ def qk_quant_inputs(q_work, k_work, cfg):
 
 def p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype, rows=None,
                    return_blasst_stats=False, qk_dequant_dtype=torch.bfloat16, scores_log2=None,
-                   return_debug=False, force_codes=None, rowmax_log2=None):
+                   return_debug=False, force_codes=None, rowmax_log2=None, rowmax_init=None):
     """``qk_dequant_dtype=torch.bfloat16`` is the reference (attention.py:534-535);
     ``torch.float32`` keeps the dequantised Q/K exact and is used only to measure
     how sensitive the reference output is to that rounding.  ``scores_log2``,
@@ -122,7 +122,9 @@ def p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype
     (rows in the reordered order of the work tensors); ``rowmax_log2``
     (B,H,G), when given, replaces the qm_k row-max estimate (log2 units, one
     value per Q group) -- used with ``scores_log2`` to replay the reference
-    algorithm on another implementation's scores and estimate."""
+    algorithm on another implementation's scores and estimate.  ``rowmax_init``
+    (B,H,S), natural-log units, rows in the work order: the reference kernel's
+    rowmax_init_bhs (attention_triton.py:127-130), passed to the attention."""
     b, s, h, d = q_work.shape
     qi, ki = qk_quant_inputs(q_work, k_work, cfg)
     qc, qs, qmeta = quant_qk(qi, cfg)
@@ -172,7 +174,7 @@ def p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype
         rowmax_est=rowmax_est, blasst_lambda=cfg.blasst_lambda, blasst_fill_mode=cfg.blasst_fill,
         blasst_fill_alpha=cfg.blasst_fill_alpha, blasst_uta_bins=cfg.blasst_uta_bins,
         return_blasst_stats=return_blasst_stats, rows=rows, return_debug=return_debug,
-        scores_log2=scores_log2, force_codes=force_codes)
+        scores_log2=scores_log2, force_codes=force_codes, rowmax_init=rowmax_init)
     res = list(res) if isinstance(res, tuple) else [res]
     res[0] = res[0].permute(*perm).contiguous().to(out_dtype)
     return res[0] if len(res) == 1 else tuple(res)
@@ -209,7 +211,7 @@ def sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype):
 
 def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=False,
                          qk_dequant_dtype=torch.bfloat16, scores_log2=None, return_debug=False,
-                         force_codes=None, rowmax_log2=None):
+                         force_codes=None, rowmax_log2=None, rowmax_init=None):
     """Output in the caller's row order.  With ``return_debug`` the debug dict of
     ``attention.attention`` (reordered row order) follows, plus ``"order"``
     (the Q k-means order, or None)."""
@@ -228,7 +230,7 @@ def fake_quant_attention(q, k, v, cfg, *, sm_scale=None, return_blasst_stats=Fal
         r = p_requant_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, out_dtype,
                            return_blasst_stats=return_blasst_stats, qk_dequant_dtype=qk_dequant_dtype,
                            scores_log2=scores_log2, return_debug=return_debug, force_codes=force_codes,
-                           rowmax_log2=rowmax_log2)
+                           rowmax_log2=rowmax_log2, rowmax_init=rowmax_init)
         r = list(r) if isinstance(r, tuple) else [r]
         o = r.pop(0)
         stats = r.pop(0) if return_blasst_stats else None

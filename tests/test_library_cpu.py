@@ -100,8 +100,16 @@ def test_kernel_config_guards():
         v(v_smooth_mode="per_block", v_smooth_block_size=32)
     with pytest.raises(ValueError, match="v_block_size .* must be >= block_n"):
         v(v_quant="fp8_block", v_fp8_block_size=32)
-    with pytest.raises(ValueError, match="p_requant_block_n=64"):
-        v(p_requant_block_n=128, p_requant_block_m=128, q_smooth_block_size=256)
+    # block_n = 128 runs; its guards follow the reference's
+    v(p_requant_block_n=128, p_requant_block_m=128, q_smooth_block_size=256)
+    with pytest.raises(ValueError, match="p_requant_block_n in"):
+        v(p_requant_block_n=32, p_requant_block_m=32)
+    with pytest.raises(ValueError, match=r"blasst UTA bins \(256\) must divide block_n \(128\)"):
+        v(p_requant_block_n=128, blasst_lambda=0.1, blasst_fill="uta256")
+    with pytest.raises(ValueError, match="v_block_size .* must be >= block_n"):
+        v(p_requant_block_n=128, v_quant="fp8_block", v_fp8_block_size=64)
+    with pytest.raises(ValueError, match="p_mx_block_n .* currently must equal block_n"):
+        v(p_requant_block_n=128, v_quant="mxfp8", p_quant="mx", p_mx_block_n=64)
     assert parse_blasst_fill("mean_a1.5", alpha=1.0, uta_bins=16) == (2, 1.5, 1)
     assert parse_blasst_fill("uta16_a1.5", alpha=1.0, uta_bins=16) == (6, 1.5, 16)
     assert parse_blasst_fill("uta", alpha=2.0, uta_bins=8) == (6, 2.0, 8)

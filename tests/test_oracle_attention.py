@@ -344,3 +344,22 @@ def test_flip_allowance_bounds_flips_of_edge_codes():
     out0, dbg0 = oattn.attention(q, k, v, vs, return_debug=True, sm_scale=LN2, p_max_offset=8,
                                  p_quant_mode="elementwise")
     assert dbg0["flip_allowance"].abs().max() == 0.0
+
+
+@pytest.mark.parametrize("block_n", [64, 128])
+def test_rowmax_init_at_the_row_max_equals_the_fixed_estimate(block_n):
+    """rowmax_init (attention_triton.py:127-130) starts the online max; at the
+    true row max the max never moves (alpha = 1), so the output equals the
+    fixed-estimate path (attention_triton.py:212-214) with the same values,
+    bit for bit; a start below every score equals the plain online max."""
+    q, k, v, v_scale = _exact_case(s=256, d=64, seed=7)
+    sm = 1.0
+    rm = (torch.matmul(q.float(), k.float().transpose(-2, -1)) * sm).amax(-1)   # (B,H,S)
+    kw = dict(sm_scale=sm, p_max_offset=8, block_m=block_n, block_n=block_n, p_quant_mode="elementwise")
+    o_init = oattn.attention(q, k, v, v_scale, rowmax_init=rm, **kw)
+    o_est = oattn.attention(q, k, v, v_scale, rowmax_est=rm, **kw)
+    assert torch.equal(o_init, o_est)
+    o_low = oattn.attention(q, k, v, v_scale, rowmax_init=torch.full_like(rm, -1e4), **kw)
+    o_online = oattn.attention(q, k, v, v_scale, **kw)
+    assert torch.equal(o_low, o_online)
+
