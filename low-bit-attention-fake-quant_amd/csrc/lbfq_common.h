@@ -108,14 +108,16 @@ __device__ __forceinline__ uint8_t quant_e4m3(float x, float sc) {
   return e4m3_encode(q);
 }
 
-// x / s for a fixed divisor s with r = 1/s (correctly rounded, computed once):
-// one product and one FMA correction of its residual (Markstein).  The result
-// is the correctly rounded quotient -- the reference's IEEE x / s -- for every
-// quotient of magnitude >= 2^-12; smaller ones encode to E4M3 zero either way.
+// x / s for a fixed divisor s > 0 with r = 1/s (correctly rounded, computed
+// once): one product and one FMA correction of its residual (Markstein).  The
+// result is the correctly rounded quotient -- the reference's IEEE x / s --
+// for every quotient of magnitude >= 2^-12; smaller ones encode to E4M3 zero
+// either way, whose sign (code 0x80 for a negative quotient) is x's: the
+// correction turns a -0 product into +0, so the sign is taken from x.
 // (Checked against IEEE division over ~2e10 cases; a reduced sweep is a CPU test.)
 __device__ __forceinline__ float div_by(float x, float s, float r) {
   const float q = x * r;
-  return fmaf(fmaf(-q, s, x), r, q);
+  return __builtin_copysignf(fmaf(fmaf(-q, s, x), r, q), x);
 }
 
 // Encode q / sc (|q / sc| <= 448 after the clamp) with the hardware RNE

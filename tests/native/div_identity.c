@@ -4,6 +4,10 @@
  * magnitude >= 2^-12.  This program checks that identity over a sweep of
  * scales (mantissas near 0, near all-ones, random) and of x at every 2^e
  * binade of the quotient from 2^-12 to 2^9, with a mantissa stride argv[1].
+ * The result carries x's sign (copysignf): for x = -0, or a product x * r
+ * that underflows to -0, the correction alone would give +0.  Quotients below
+ * 2^-12 (x = +-0, denormal and tiny x) must encode to E4M3 zero on both sides
+ * (magnitude < 2^-10) with the same sign.
  * Exit status 0 iff no mismatch. */
 #include <math.h>
 #include <stdint.h>
@@ -35,13 +39,31 @@ int main(int argc, char** argv) {
         for (uint32_t sg = 0; sg < 2; ++sg) {
           const float x = fu((sg << 31) | (be << 23) | m);
           const float q = x * r;
-          const float q1 = fmaf(fmaf(-q, s, x), r, q);
+          const float q1 = copysignf(fmaf(fmaf(-q, s, x), r, q), x);
           const float ex = x / s;
           ++tot;
           if (uf(q1) != uf(ex)) {
             if (bad < 5) printf("mismatch s=%a x=%a got=%a want=%a\n", s, x, q1, ex);
             ++bad;
           }
+        }
+      }
+    }
+    /* zero, denormal and tiny x: quotients below 2^-12 */
+    for (int k = -1; k < 300; ++k) {
+      uint32_t mag;
+      if (k < 0) mag = 0u;                                   /* +-0 */
+      else if (k < 100) mag = (uint32_t)(rand() & 0x7fffff); /* denormals */
+      else mag = (uf(s * ldexpf(1.0f, -13 - (k % 40))) & 0x7f800000u) | ((uint32_t)rand() & 0x7fffff);
+      for (uint32_t sg = 0; sg < 2; ++sg) {
+        const float x = fu((sg << 31) | mag);
+        const float q = x * r;
+        const float q1 = copysignf(fmaf(fmaf(-q, s, x), r, q), x);
+        const float ex = x / s;
+        ++tot;
+        if (signbit(q1) != signbit(ex) || fabsf(q1) >= 0x1p-10f || fabsf(ex) >= 0x1p-10f) {
+          if (bad < 5) printf("small-quotient mismatch s=%a x=%a got=%a want=%a\n", s, x, q1, ex);
+          ++bad;
         }
       }
     }

@@ -15,6 +15,13 @@ DTYPES = [torch.bfloat16, torch.float16, torch.float32]
 def _inputs(shape, dtype, seed):
     x = cpu_randn(*shape, seed=seed, dtype=torch.float32, scale=2.0)
     x[..., 3] *= 20.0  # an outlier channel
+    # signed zeros and values far below the E4M3 range: their codes are
+    # +-0 with the sign of x (0x80 for a negative quotient)
+    f = x.view(-1)
+    f[::97] = -0.0
+    f[1::101] = 0.0
+    f[2::103] = -1e-30
+    f[3::107] = 1e-30
     return x.to(dtype)
 
 
