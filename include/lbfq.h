@@ -151,7 +151,11 @@ int lbfq_qmk_kquant(const float* qm, const void* ks, int ks_dtype, const int32_t
  * FP8 codes + scales instead of pre-dequantised bf16 tensors. */
 typedef struct {
   int64_t B, H, S, D;             /* S queries == S keys; D in {64, 128}          */
-  int64_t s_pitch;                /* rows of the code buffers, multiple of 128     */
+  int64_t s_pitch;                /* rows of the code buffers, multiple of 128;    */
+                                  /* rows [S, s_pitch) of the Q/K codes and columns*/
+                                  /* [S, s_pitch) of V^T must hold finite codes    */
+                                  /* (the package writes zeros): the masked keys of*/
+                                  /* the last tile are read and multiplied by P = 0*/
   const uint8_t* q_codes;         /* (B,H,s_pitch,D)                               */
   const uint8_t* k_codes;         /* (B,H,s_pitch,D)                               */
   const uint8_t* v_codes_t;       /* (B,H,D,s_pitch)                               */
