@@ -1058,6 +1058,15 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN))
 #pragma unroll
     for (int i = 0; i < NQK; ++i) ke_n[i] = qk_scale(nxt, i);
     const float vsc = vmeta[vcur].vsc[0];
+    // ELIDE: the PV MFMAs of tile it-1 are skipped (wave-uniform branch) when
+    // all of its P codes in the wave are zero -- an elided tile (below) leaves
+    // zero codes; the product would add exact zeros
+    bool pv_zero = false;
+    if constexpr (ELIDE) {
+      const int nz = (pop_prev[0] | pop_prev[1] | pop_prev[2] | pop_prev[3]) |
+                     (pop_prev[4] | pop_prev[5] | pop_prev[6] | pop_prev[7]);
+      pv_zero = __all(nz == 0);
+    }
     v8i va[2], ka[2];
     va[0] = pv_read(vprev, 0);
     ka[0] = qk_read(nxt, 0);
@@ -1218,7 +1227,7 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN))
         v8i vac = va[c & 1];
         pin(vac);
         if (c + 1 < NDB) va[(c + 1) & 1] = pv_read(vprev, c + 1);
-        pv_mfma(c, vac, pop_prev, pe_prev, ve_p[c]);
+        if (!pv_zero) pv_mfma(c, vac, pop_prev, pe_prev, ve_p[c]);
       }
       if (VALPHA && c == 1) {  // row sums of the codes of tile it-1 (every register holds the lane's)
         const v16f zero = {};
@@ -1327,10 +1336,9 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN))
     // one fill code on all 64 keys and the tile's PV product is that code times
     // the column sums of V.  It is added here in fp32, in the units of the
     // current sigma (alpha is 1 for a skipped row, so nothing is rescaled),
-    // and the tile's P codes are left at zero, so the PV MFMAs that the next
-    // step issues for it add nothing.  (Skipping those MFMAs with a branch,
-    // or with a second step variant, needs a loop-carried flag; the kernel
-    // then exceeds 256 VGPRs and spills.)
+    // and the tile's P codes are left at zero, so the next step skips the
+    // tile's PV MFMAs (pv_zero; a flag carried from this step instead takes
+    // the kernel past 256 VGPRs).
     const bool elide = ELIDE && !MASKED && skip_all && a.vcol != nullptr;
     // an elided tile keeps sigma (f = 1: no rescale)
     const float sig_keep = elide ? sigma : sig_new;
