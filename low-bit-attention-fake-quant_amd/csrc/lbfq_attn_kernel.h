@@ -1381,11 +1381,12 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN))
   {
     // four steps per iteration: ring slots are constants, and the loop-carried
     // scores, P codes and scale registers rotate through the unrolled steps
-    // instead of being copied at the back edge.  Kernels with BLASST or V
-    // smoothing carry more state through a step; unrolled, they need more
-    // than the 256 VGPRs of two waves per SIMD and spill inside the loop, so
-    // they run one step per iteration (ring slots then come from it % 4).
-    constexpr bool UNROLL = !BLASST && !VALPHA;
+    // instead of being copied at the back edge.  Kernels that carry more
+    // state through a step -- V smoothing, the packed UTA fill codes, the
+    // per-row fills with MX Q/K -- need more than the 256 VGPRs of two waves
+    // per SIMD when unrolled and spill inside the loop, so they run one step
+    // per iteration (ring slots then come from it % 4).
+    constexpr bool UNROLL = !VALPHA && (BL == 0 || BL == 3 || (BL == 1 && !QK_MX));
     int it0 = 0;
     if constexpr (UNROLL) {
       for (; it0 + 3 < nfull; it0 += 4) {
