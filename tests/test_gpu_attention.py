@@ -437,3 +437,42 @@ def test_blasst_elided_tiles_match_the_mfma_path(gpu):
         d = (out.float() - ref.float()).abs()
         print(f"{fill}/{p_quant}: elided wave tiles {int(wt[..., 0].sum())}, elided vs MFMA path max|diff| "
               f"{d.max().item():.3e}, {int((d > 0).sum())} of {d.numel()} outputs differ")
+
+
+BATCH_CASES = {
+    "dense_qmk_kmeans": dict(qk_quant="fp8_block", fp8_block_size=64, smoothing="full", q_smooth_block_size=256,
+                             q_kmeans_k=16, p_quant="dynamic", rowmax_mode="qm_k"),
+    "dense_online": dict(qk_quant="fp8_block", fp8_block_size=128, v_quant="fp8_channel", smoothing="full",
+                         q_smooth_block_size=128, q_kmeans_k=None, p_quant="dynamic"),
+    "blasst_mean_elided": dict(qk_quant="fp8_block", fp8_block_size=64, smoothing="full", q_smooth_block_size=256,
+                               q_kmeans_k=16, p_quant="dynamic", rowmax_mode="qm_k", blasst_lambda=0.05,
+                               blasst_fill="mean_a1.5"),
+    "blasst_uta16": dict(qk_quant="fp8_block", fp8_block_size=64, smoothing="full", q_smooth_block_size=256,
+                         q_kmeans_k=16, p_quant="dynamic", rowmax_mode="qm_k", blasst_lambda=0.05,
+                         blasst_fill="uta16_a1.5"),
+    "blasst_block128_mx": dict(qk_quant="mxfp8", v_quant="mxfp8", v_mxfp8_block_size=128, smoothing="k_only",
+                               q_kmeans_k=None, p_quant="mx", p_mx_block_n=128, p_requant_block_n=128,
+                               blasst_lambda=0.05, blasst_fill="logn"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(BATCH_CASES))
+def test_batch_of_two_matches_oracle(gpu, name):
+    """B = 2 with different inputs per batch entry: every per-(batch, head)
+    table (Q/K/V codes and scales, permutations, qmk bias, V column sums,
+    BLASST counters) is indexed by b*H + h; the pair must meet the strict
+    bound against the replay, and each entry must equal the same configuration
+    run on that entry alone bit for bit.  (With k-means the centroid seeds
+    are drawn per slice index b*H + h, so only entry 0 shares its seeds with a
+    single run.)"""
+    from low_bit_fake_quant import fake_quant_attention
+    cfg = _cfg(**BATCH_CASES[name])
+    parts = [_inputs(n=1024, seed=30 + i, q_clusters=4, v_bias=True, field=(4, 16, 16)) for i in range(2)]
+    q, k, v = (torch.cat([p[j] for p in parts], 0) for j in range(3))
+    out = fake_quant_attention(q.to(gpu), k.to(gpu), v.to(gpu), cfg).cpu()
+    check_parity(out, q, k, v, cfg, f"batch2-{name}")
+    for i, (qi, ki, vi) in enumerate(parts):
+        if i > 0 and cfg.q_kmeans_k is not None:
+            continue
+        one = fake_quant_attention(qi.to(gpu), ki.to(gpu), vi.to(gpu), cfg).cpu()
+        assert torch.equal(one, out[i:i + 1]), f"{name}: batch entry {i} differs from its single run"
