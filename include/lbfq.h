@@ -53,7 +53,9 @@ const char* lbfq_last_error(void);
  * the work tensor); the Hadamard rotation hadamard.py:77-117; and the
  * reorder gathers kmeans.py:88-89 / :127-135 (gather != NULL).
  * Per element: x[gather[s]] - sub -> round to x_dtype -> (signs, FWHT,
- * *had_scale, round) -> quantise.  One tile = R rows of one (b, h). */
+ * *had_scale, round) -> quantise.  One tile = R rows of one (b, h).  The
+ * Hadamard rotation goes with quant modes NONE, FP8_BLOCK and MX_QK only
+ * (it rotates Q/K); S and the code pitch must be below 2^31. */
 typedef struct {
   const void* x; int x_dtype;              /* input, NHD                        */
   int64_t B, S, H, D;                      /* D in {64, 128}                    */

@@ -57,6 +57,8 @@ struct RowTileArgs {
   int mx_block;
   int smoothed_stage;
   int scale_e8m0;
+  uint32_t ntile;  // ceil(S / R)
+  uint32_t nsub;   // S / sub_block (BLOCKVEC)
 };
 
 __device__ __forceinline__ void load8(const void* x, int dt, int64_t idx, float v[8]) {
@@ -121,6 +123,24 @@ __device__ __forceinline__ void load8t(const void* x, int64_t idx, float v[8]) {
 }
 
 template <int DT>
+__device__ __forceinline__ void load8p(const uint8_t* p, float v[8]) {
+  if constexpr (DT == kF32) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xffffu), hi = static_cast<uint16_t>(w[i] >> 16);
+      if constexpr (DT == kBF16) { v[2 * i] = bf16_bits_to_f32(lo); v[2 * i + 1] = bf16_bits_to_f32(hi); }
+      else { v[2 * i] = f16_bits_to_f32(lo); v[2 * i + 1] = f16_bits_to_f32(hi); }
+    }
+  }
+}
+
+template <int DT>
 __device__ __forceinline__ float round_dt(float v) {
   if constexpr (DT == kBF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
   else if constexpr (DT == kF16) return f16_bits_to_f32(f32_to_f16_bits(v));
@@ -128,167 +148,209 @@ __device__ __forceinline__ float round_dt(float v) {
 }
 
 
-// ---- one wave per R-row tile ------------------------------------------------
-// A wave owns one (b, h, R-row tile): lane l holds columns d0 = 8 (l % (D/8))
-// .. d0+7 of rows rl, rl + rpw, rl + 2 rpw, ... (rpw = 64 / (D/8) rows per wave
-// pass).  Tile reductions (block amax, per-column amax) are wave reductions,
-// so a tile needs no LDS round trip and no barrier; four waves of a workgroup
-// take four adjacent (head-fastest) tiles.  A tile of up to kNpMax passes
-// whose scale depends on the whole tile stays in registers (16-bit inputs as
-// packed halves: after the transforms every value is representable in the
-// input dtype), so it is read from memory once.  Loads are issued kLB passes
-// at a time, all in flight before any is used.
+// ---- one workgroup per R-row tile ------------------------------------------
+// A workgroup of four waves owns one (b, h, R-row tile).  A pass covers
+// rpw = 64 / (D/8) rows: lane l holds columns d0 = 8 (l % (D/8)) .. d0+7 of
+// row rl = l / (D/8) of the pass.  Wave w takes passes w, w + 4, w + 8, ..., so
+// at every step the four waves read 4 rpw adjacent rows.  Tile reductions
+// (block amax, per-column amax) are wave reductions followed by one LDS
+// exchange.  A tile of up to 4 kKeep passes whose scale depends on the whole
+// tile stays in registers (fp32), so it is read from memory once; a longer one
+// is read twice.  Transposed (BHDS) codes go through an LDS stage of
+// kStageRows rows that all 256 threads write out as dwords of four
+// consecutive keys.  Consecutive workgroups take adjacent heads of one row
+// tile (adjacent 16-byte pieces of the same rows).  SUB (a mean is
+// subtracted) and HAD (FWHT) are compile-time so that the common cases carry
+// no per-element work for the others; the kernel is VALU-issue-bound.
 constexpr int kTileWaves = 4;
-constexpr int kNpMax = 16;
-constexpr int kLB = 4;
-constexpr int kStageRows = 64;  // rows per BHDS staging chunk (per wave)
+constexpr int kKeep = 4;        // resident passes per wave
+constexpr int kLB = 4;          // passes per wave in flight when streaming
+constexpr int kStageRows = 64;  // rows per BHDS staging chunk
 
-template <int DT>
-struct TileStore {  // resident tile values of one lane
-  uint32_t w[kNpMax][4];
-  __device__ __forceinline__ void put(int p, const float v[8]) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint32_t lo, hi;
-      if constexpr (DT == kBF16) { lo = f32_to_bf16_bits(v[2 * k]); hi = f32_to_bf16_bits(v[2 * k + 1]); }
-      else { lo = f32_to_f16_bits(v[2 * k]); hi = f32_to_f16_bits(v[2 * k + 1]); }
-      w[p][k] = lo | (hi << 16);
-    }
-  }
-  __device__ __forceinline__ void get(int p, float v[8]) const {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint16_t lo = static_cast<uint16_t>(w[p][k] & 0xffffu), hi = static_cast<uint16_t>(w[p][k] >> 16);
-      if constexpr (DT == kBF16) { v[2 * k] = bf16_bits_to_f32(lo); v[2 * k + 1] = bf16_bits_to_f32(hi); }
-      else { v[2 * k] = f16_bits_to_f32(lo); v[2 * k + 1] = f16_bits_to_f32(hi); }
-    }
-  }
-};
-template <>
-struct TileStore<kF32> {
-  float f[kNpMax][8];
-  __device__ __forceinline__ void put(int p, const float v[8]) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) f[p][k] = v[k];
-  }
-  __device__ __forceinline__ void get(int p, float v[8]) const {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = f[p][k];
-  }
-};
-
-template <int DT, int QM>
+template <int DT, int QM, bool SUB, bool HAD>
 __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a) {
   constexpr bool TILE_RED = QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_MX_V || QM == LBFQ_Q_CHANNEL_AMAX;
   constexpr bool RESIDENT_MODE = QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_MX_V;
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  constexpr int ES = DT == kF32 ? 4 : 2;  // input element bytes
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // wave-uniform (scalar): the per-wave pass counts below stay scalar, so pass
+  // guards are branches, not exec masks that serialise the loads
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lpr = static_cast<int>(a.D / 8);  // lanes per row
   const int rpw = 64 / lpr;                   // rows per wave pass
   const int d0 = (lane % lpr) * 8;
   const int rl = lane / lpr;
 
-  const int64_t ntile = (a.S + a.R - 1) / a.R;
-  int64_t t = static_cast<int64_t>(blockIdx.x) * kTileWaves + wv;
-  if (t >= a.B * a.H * ntile) return;  // whole wave
-  const int64_t h = t % a.H; t /= a.H;
+  // 32-bit index arithmetic: the grid (B * H * ntile workgroups, exactly) is
+  // below 2^31
+  const uint32_t ntile = a.ntile;
+  const uint32_t H32 = static_cast<uint32_t>(a.H);
+  uint32_t t = blockIdx.x;
+  const int64_t h = t % H32;
+  t /= H32;
   const int64_t tile = t % ntile;
   const int64_t b = t / ntile;
   const int64_t bh = b * a.H + h;
   const int64_t s0 = tile * a.R;
-  const int np = a.R / rpw;  // passes of the tile (R is a multiple of rpw)
+  const int np = a.R / rpw;                                     // passes of the tile (R is a multiple of rpw)
+  const int npw_max = (np + kTileWaves - 1) / kTileWaves;       // passes of wave 0 (the most)
+  const int npw = np > wv ? (np - wv + kTileWaves - 1) / kTileWaves : 0;  // passes of this wave
+  const int nvalid = a.S - s0 < a.R ? static_cast<int>(a.S - s0) : a.R;  // rows of the tile below S
+  // every pass of every wave holds valid rows (no zeroing needed)
+  const bool tile_full = nvalid == a.R && np % kTileWaves == 0;
   const int tcp = static_cast<int>(a.D) + 4;
-  extern __shared__ uint8_t stage_all[];  // BHDS staging: per wave kStageRows rows of tcp bytes
-  uint8_t* stage = stage_all + wv * kStageRows * tcp;
+  const bool bhds = a.codes_layout == LBFQ_LAYOUT_BHDS;
+  const int ipc = kStageRows / rpw / kTileWaves;                // passes per wave and staging chunk
 
-  // ---- load + transform passes [p0, p0 + kLB) -------------------------------
-  float v[kLB][8];
-  bool ok[kLB];
-  auto load_group = [&](int p0, bool store_smoothed) {
-    int64_t src[kLB];
-#pragma unroll
-    for (int i = 0; i < kLB; ++i) {
-      const int64_t s = s0 + (p0 + i) * rpw + rl;
-      ok[i] = p0 + i < np && s < a.S;
-      src[i] = ok[i] ? s : s0;  // a safe row (not used) past the tile
-      if (a.gather) src[i] = a.gather[bh * a.S + src[i]];
+  // Per-tile bases; a row offset within one (b, h) is a 32 x 32 -> 64-bit
+  // product (S, H * D and the code pitch are below 2^31, checked on the host).
+  const uint32_t hd = static_cast<uint32_t>(a.H * a.D);
+  const uint8_t* xlane = static_cast<const uint8_t*>(a.x) + ((b * a.S * a.H + h) * a.D + d0) * ES;
+  const uint32_t x_row_bytes = hd * ES;
+  const int32_t* gath = a.gather ? a.gather + bh * a.S : nullptr;
+  // the subtracted mean row: one per tile for COLVEC and for a BLOCKVEC group
+  // that holds the whole tile (sub_block a multiple of R), else one per pass
+  bool sub_fixed = true;
+  const float* sub_lane = nullptr;
+  float mfix[8];
+  if constexpr (SUB) {
+    sub_fixed = a.sub_mode == LBFQ_SUB_COLVEC || a.sub_block % a.R == 0;
+    sub_lane = a.sub_mode == LBFQ_SUB_COLVEC ? a.sub + bh * a.D + d0 : a.sub + (b * a.nsub * a.H + h) * a.D + d0;
+    if (sub_fixed) {
+      const float* m = sub_lane + (a.sub_mode == LBFQ_SUB_BLOCKVEC
+                                       ? static_cast<uint64_t>(static_cast<uint32_t>(s0) / static_cast<uint32_t>(a.sub_block)) * hd
+                                       : 0);
+      const float4 m0 = reinterpret_cast<const float4*>(m)[0], m1 = reinterpret_cast<const float4*>(m)[1];
+      mfix[0] = m0.x; mfix[1] = m0.y; mfix[2] = m0.z; mfix[3] = m0.w;
+      mfix[4] = m1.x; mfix[5] = m1.y; mfix[6] = m1.z; mfix[7] = m1.w;
     }
+  }
+  const bool sm0 = a.smoothed && a.smoothed_stage == 0, sm1 = a.smoothed && a.smoothed_stage == 1;
+  __shared__ float red[kTileWaves][128];  // cross-wave reductions (D <= 128)
+  extern __shared__ uint8_t stage[];      // BHDS staging: kStageRows rows of tcp bytes
+
+  // ---- load + transform -----------------------------------------------------
+  // source row of pass p (a row >= nvalid reads the tile's first row, unused)
+  auto pass_src = [&](int p) -> uint32_t {
+    const int r = p * rpw + rl;
+    uint32_t src = static_cast<uint32_t>(s0 + (r < nvalid ? r : 0));
+    if (gath) src = static_cast<uint32_t>(gath[src]);
+    return src;
+  };
+  auto load_pass = [&](uint32_t src, float (&x)[8]) {
+    load8p<DT>(xlane + static_cast<uint64_t>(src) * x_row_bytes, x);
+  };
+  // subtract, zero rows past the tile, optional smoothed copy, optional FWHT
+  auto transform = [&](int p, float (&x)[8], bool store_smoothed) {
+    const int r = p * rpw + rl;
+    const bool okp = r < nvalid;
+    const int64_t s_out = s0 + (okp ? r : 0);
+    if constexpr (SUB) {
+      float mm[8];
+      if (sub_fixed) {
 #pragma unroll
-    for (int i = 0; i < kLB; ++i) load8t<DT>(a.x, ((b * a.S + src[i]) * a.H + h) * a.D + d0, v[i]);
-#pragma unroll
-    for (int i = 0; i < kLB; ++i) {
-      const int64_t s_out = ok[i] ? s0 + (p0 + i) * rpw + rl : s0;
-      if (a.sub_mode != LBFQ_SUB_NONE) {
-        const float* m = a.sub_mode == LBFQ_SUB_COLVEC
-                             ? a.sub + bh * a.D + d0
-                             : a.sub + ((b * (a.S / a.sub_block) + s_out / a.sub_block) * a.H + h) * a.D + d0;
+        for (int k = 0; k < 8; ++k) mm[k] = mfix[k];
+      } else {
+        const float* m = sub_lane + static_cast<uint64_t>(static_cast<uint32_t>(s_out) /
+                                                          static_cast<uint32_t>(a.sub_block)) * hd;
         const float4 m0 = reinterpret_cast<const float4*>(m)[0], m1 = reinterpret_cast<const float4*>(m)[1];
-        const float mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[i][k] = round_dt<DT>(v[i][k] - mm[k]);
+        mm[0] = m0.x; mm[1] = m0.y; mm[2] = m0.z; mm[3] = m0.w;
+        mm[4] = m1.x; mm[5] = m1.y; mm[6] = m1.z; mm[7] = m1.w;
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[i][k] = ok[i] ? v[i][k] : 0.0f;
-      if (store_smoothed && ok[i] && a.smoothed && a.smoothed_stage == 0)
-        store8(a.smoothed, DT, ((b * a.S + s_out) * a.H + h) * a.D + d0, v[i]);
-      if (a.hadamard) {
-        if (a.signs) {
-          const int8_t* sg = a.signs + h * a.D + d0;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) v[i][k] = sg[k] < 0 ? -v[i][k] : v[i][k];
-        }
-#pragma unroll
-        for (int st = 1; st < 8; st <<= 1) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            if ((k & st) == 0) {
-              const float l = v[i][k], rr = v[i][k + st];
-              v[i][k] = l + rr;
-              v[i][k + st] = l - rr;
-            }
-          }
-        }
-        // cross-lane stages: stride 8, 16, ... within the row's lpr lanes
-        for (int m = 1; m < lpr; m <<= 1) {
-          const bool upper = (lane & m) != 0;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const float o = __shfl_xor(v[i][k], m, 64);
-            v[i][k] = upper ? (o - v[i][k]) : (v[i][k] + o);
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[i][k] = round_dt<DT>(v[i][k] * a.had_scale);
-        if (store_smoothed && ok[i] && a.smoothed && a.smoothed_stage == 1)
-          store8(a.smoothed, DT, ((b * a.S + s_out) * a.H + h) * a.D + d0, v[i]);
-      }
+      for (int k = 0; k < 8; ++k) x[k] = round_dt<DT>(x[k] - mm[k]);
     }
+    if (!tile_full) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = okp ? x[k] : 0.0f;
+    }
+    if (store_smoothed && sm0 && okp) store8(a.smoothed, DT, ((b * a.S + s_out) * a.H + h) * a.D + d0, x);
+    if constexpr (HAD) {
+      if (a.signs) {
+        const int8_t* sg = a.signs + h * a.D + d0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = sg[k] < 0 ? -x[k] : x[k];
+      }
+#pragma unroll
+      for (int st = 1; st < 8; st <<= 1) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if ((k & st) == 0) {
+            const float l = x[k], rr = x[k + st];
+            x[k] = l + rr;
+            x[k + st] = l - rr;
+          }
+        }
+      }
+      // cross-lane stages: stride 8, 16, ... within the row's lpr lanes
+      for (int m = 1; m < lpr; m <<= 1) {
+        const bool upper = (lane & m) != 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float o = __shfl_xor(x[k], m, 64);
+          x[k] = upper ? (o - x[k]) : (x[k] + o);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = round_dt<DT>(x[k] * a.had_scale);
+      if (store_smoothed && sm1 && okp) store8(a.smoothed, DT, ((b * a.S + s_out) * a.H + h) * a.D + d0, x);
+    }
+  };
+  // this wave's passes i0 .. i0 + kLB - 1 (pass p = wv + 4 i): every load in
+  // flight before the first transform
+  float v[kLB][8];
+  auto load_group = [&](int i0, bool store_smoothed) {
+    uint32_t src[kLB];
+#pragma unroll
+    for (int i = 0; i < kLB; ++i) src[i] = pass_src(wv + kTileWaves * (i0 + i));
+#pragma unroll
+    for (int i = 0; i < kLB; ++i) load_pass(src[i], v[i]);
+#pragma unroll
+    for (int i = 0; i < kLB; ++i) transform(wv + kTileWaves * (i0 + i), v[i], store_smoothed);
   };
 
   // ---- quantise one pass and write its codes -------------------------------
   float sc8[8], rc8[8];  // per-column scale and reciprocal (block: all equal)
+  // NHD / BHSD codes of row s at crow + s * cstride
+  const bool nhd = a.codes_layout == LBFQ_LAYOUT_NHD;
+  uint8_t* const crow = nhd ? a.codes + (b * a.S * a.H + h) * a.D + d0 : a.codes + bh * a.codes_spitch * a.D + d0;
+  const uint32_t cstride = nhd ? hd : static_cast<uint32_t>(a.D);
+  uint8_t* const codes_bhds = a.codes + bh * a.D * a.codes_spitch + s0;  // + d * pitch + r
+  // rows [r0, r0 + nrows) of the tile are staged: all threads write them
+  // transposed, each packing 4 consecutive keys of one d into a dword
   auto flush_stage = [&](int r0, int nrows) {
-    // rows [r0, r0 + nrows) of the tile are staged: write them transposed, each
-    // lane packing 4 consecutive keys of one d into a dword
-    const int64_t nvalid_all = a.S - s0 < a.R ? a.S - s0 : a.R;
-    const int64_t nvalid = nvalid_all - r0 < nrows ? nvalid_all - r0 : nrows;
+    const int nv = nvalid - r0 < nrows ? nvalid - r0 : nrows;
+    const uint32_t pitch = static_cast<uint32_t>(a.codes_spitch);
+    if (nv == kStageRows) {  // a full chunk: 16 dwords per code row
+      constexpr int rq = kStageRows / 4;
+      for (int e = tid; e < a.D * rq; e += kTileWaves * 64) {
+        const int d = e / rq, r = (e % rq) * 4;
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w |= static_cast<uint32_t>(stage[(r + k) * tcp + d]) << (8 * k);
+        *reinterpret_cast<uint32_t*>(codes_bhds + static_cast<uint64_t>(static_cast<uint32_t>(d)) * pitch + r0 + r) = w;
+      }
+      return;
+    }
     const int rq = nrows / 4;
-    for (int e = lane; e < a.D * rq; e += 64) {
+    for (int e = tid; e < a.D * rq; e += kTileWaves * 64) {
       const int d = e / rq, r = (e - d * rq) * 4;
-      uint8_t* dst = a.codes + (bh * a.D + d) * a.codes_spitch + s0 + r0 + r;
-      if (r + 4 <= nvalid) {
+      uint8_t* dst = codes_bhds + static_cast<uint64_t>(static_cast<uint32_t>(d)) * pitch + r0 + r;
+      if (r + 4 <= nv) {
         uint32_t w = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) w |= static_cast<uint32_t>(stage[(r + k) * tcp + d]) << (8 * k);
         *reinterpret_cast<uint32_t*>(dst) = w;
       } else {
-        for (int k = 0; r + k < nvalid; ++k) dst[k] = stage[(r + k) * tcp + d];
+        for (int k = 0; r + k < nv; ++k) dst[k] = stage[(r + k) * tcp + d];
       }
     }
   };
-  auto quant_pass = [&](int p, const float x[8], bool valid) {
+  auto quant_pass = [&](int p, const float (&x)[8]) {
     const int r = p * rpw + rl;
-    const int64_t s = s0 + r;
+    const bool valid = r < nvalid;
+    const uint32_t s = static_cast<uint32_t>(s0 + r);
     float q[8];
     if constexpr (QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_CHANNEL) {
 #pragma unroll
@@ -308,28 +370,28 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
 #pragma unroll
       for (int k = 0; k < 8; ++k) q[k] = clamp448(x[k] * inv);
       if (valid && (lane & (ml - 1)) == 0) {
-        const int64_t si = b * a.sc_b + s * a.sc_s + h * a.sc_h + (d0 / a.mx_block) * a.sc_d;
+        const int64_t si = b * a.sc_b + static_cast<int64_t>(s) * a.sc_s + h * a.sc_h + (d0 / a.mx_block) * a.sc_d;
         if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
         else a.scale[si] = sc;
       }
     }
     const uint32_t lo = cvt4_e4m3(q), hi = cvt4_e4m3(q + 4);
-    if (a.codes_layout == LBFQ_LAYOUT_BHDS) {
+    if (bhds) {
       uint32_t* st = reinterpret_cast<uint32_t*>(stage + (r % kStageRows) * tcp + d0);
       st[0] = lo;
       st[1] = hi;
     } else if (valid) {
-      if (a.codes_layout == LBFQ_LAYOUT_NHD)
-        *reinterpret_cast<uint2*>(a.codes + ((b * a.S + s) * a.H + h) * a.D + d0) = make_uint2(lo, hi);
-      else
-        *reinterpret_cast<uint2*>(a.codes + (bh * a.codes_spitch + s) * a.D + d0) = make_uint2(lo, hi);
+      *reinterpret_cast<uint2*>(crow + static_cast<uint64_t>(s) * cstride) = make_uint2(lo, hi);
     }
   };
-  const int spc = kStageRows / rpw;  // passes per staging chunk
-  auto after_pass = [&](int p) {     // BHDS: flush a full (or the last) staging chunk
-    if (a.codes_layout == LBFQ_LAYOUT_BHDS && ((p + 1) % spc == 0 || p + 1 == np)) {
-      const int r0 = (p / spc) * kStageRows;
-      flush_stage(r0, (p + 1) * rpw - r0);
+  // after this wave's pass i (every wave reaches the same i): BHDS writes out
+  // a complete staging chunk, or the last one
+  auto after_pass = [&](int i) {
+    if (bhds && ((i + 1) % ipc == 0 || i + 1 == npw_max)) {
+      const int c = i / ipc;
+      __syncthreads();
+      flush_stage(c * kStageRows, np * rpw - c * kStageRows < kStageRows ? np * rpw - c * kStageRows : kStageRows);
+      __syncthreads();
     }
   };
 
@@ -341,7 +403,7 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
       sc8[k] = __uint_as_float(tb[k]) / kFp8Max;
       rc8[k] = 1.0f / sc8[k];
     }
-    if (tile == 0 && rl == 0 && a.scale) {
+    if (tile == 0 && wv == 0 && rl == 0 && a.scale) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) a.scale[b * a.sc_b + h * a.sc_h + (d0 + k) * a.sc_d] = sc8[k];
     }
@@ -349,52 +411,68 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
 
   if constexpr (TILE_RED) {
     // ---- reductions over the tile (resident: keep the values) ---------------
-    const bool resident = RESIDENT_MODE && np <= kNpMax;
-    TileStore<DT> keep;
+    const bool resident = RESIDENT_MODE && npw_max <= kKeep;
+    float keep[kKeep][8];
     float tmax = 0.0f, cmax[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) cmax[k] = 0.0f;
-    auto reduce_group = [&]() {
+    auto reduce_pass = [&](const float (&x)[8]) {
 #pragma unroll
-      for (int i = 0; i < kLB; ++i) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float av = fabsf(v[i][k]);  // zero for rows past the tile
-          tmax = fmaxf(tmax, av);
-          cmax[k] = fmaxf(cmax[k], av);
-        }
+      for (int k = 0; k < 8; ++k) {
+        const float av = fabsf(x[k]);  // zero for rows past the tile
+        if constexpr (QM == LBFQ_Q_FP8_BLOCK) tmax = fmaxf(tmax, av);
+        else cmax[k] = fmaxf(cmax[k], av);
       }
     };
     if (resident) {
-      // pass groups at compile-time offsets, so the kept values stay in registers
+      // compile-time pass slots, so the kept values stay in registers; every
+      // slot is loaded (a slot past this wave's passes reads a safe row and is
+      // not used), so all loads are in flight together
+      uint32_t src[kKeep];
 #pragma unroll
-      for (int g = 0; g < kNpMax / kLB; ++g) {
-        if (g * kLB < np) {
-          load_group(g * kLB, true);
-          reduce_group();
+      for (int i = 0; i < kKeep; ++i) src[i] = pass_src(wv + kTileWaves * i);
 #pragma unroll
-          for (int i = 0; i < kLB; ++i) keep.put(g * kLB + i, v[i]);
+      for (int i = 0; i < kKeep; ++i) load_pass(src[i], keep[i]);
+#pragma unroll
+      for (int i = 0; i < kKeep; ++i) {
+        if (i < npw) {
+          transform(wv + kTileWaves * i, keep[i], true);
+          reduce_pass(keep[i]);
         }
       }
     } else {
-      for (int p0 = 0; p0 < np; p0 += kLB) {
-        load_group(p0, QM == LBFQ_Q_CHANNEL_AMAX);
-        reduce_group();
+      for (int i0 = 0; i0 < npw; i0 += kLB) {
+        load_group(i0, QM == LBFQ_Q_CHANNEL_AMAX);
+#pragma unroll
+        for (int i = 0; i < kLB; ++i)
+          if (i0 + i < npw) reduce_pass(v[i]);
       }
     }
     if constexpr (QM == LBFQ_Q_FP8_BLOCK) {
-      const float m = fmaxf(wave_max(tmax), kAmaxFloor);
+      const float wm = wave_max(tmax);
+      if (lane == 0) red[wv][0] = wm;
+      __syncthreads();
+      const float m = fmaxf(fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0])), kAmaxFloor);
       const float sc = m / kFp8Max, rc = 1.0f / sc;
 #pragma unroll
       for (int k = 0; k < 8; ++k) { sc8[k] = sc; rc8[k] = rc; }
-      if (lane == 0) a.scale[b * a.sc_b + tile * a.sc_s + h * a.sc_h] = sc;
+      if (tid == 0) a.scale[b * a.sc_b + tile * a.sc_s + h * a.sc_h] = sc;
     } else {
-      // per-column max over the tile: lanes with equal d0 hold the same columns
+      // per-column max over the tile: lanes with equal d0 hold the same
+      // columns, then the four waves' maxima
 #pragma unroll
       for (int k = 0; k < 8; ++k)
         for (int m = lpr; m < 64; m <<= 1) cmax[k] = fmaxf(cmax[k], __shfl_xor(cmax[k], m, 64));
+      if (rl == 0) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) red[wv][d0 + k] = cmax[k];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        cmax[k] = fmaxf(fmaxf(red[0][d0 + k], red[1][d0 + k]), fmaxf(red[2][d0 + k], red[3][d0 + k]));
       if constexpr (QM == LBFQ_Q_CHANNEL_AMAX) {
-        if (rl == 0) {
+        if (wv == 0 && rl == 0) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) atomicMax(a.amax_table + bh * a.D + d0 + k, __float_as_uint(cmax[k]));
         }
@@ -405,7 +483,7 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
           const float sc = mx_scale_from_amax(fmaxf(cmax[k], kAmaxFloor));
           sc8[k] = sc;
           rc8[k] = 1.0f / sc;  // exact: 2^-e
-          if (rl == 0) {
+          if (wv == 0 && rl == 0) {
             const int64_t si = b * a.sc_b + tile * a.sc_s + h * a.sc_h + (d0 + k) * a.sc_d;
             if (a.scale_e8m0) reinterpret_cast<uint8_t*>(a.scale)[si] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
             else a.scale[si] = sc;
@@ -415,12 +493,10 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
     }
     if (resident) {
 #pragma unroll
-      for (int p = 0; p < kNpMax; ++p) {
-        if (p < np) {
-          float x[8];
-          keep.get(p, x);
-          quant_pass(p, x, s0 + p * rpw + rl < a.S);
-          after_pass(p);
+      for (int i = 0; i < kKeep; ++i) {
+        if (i < npw_max) {
+          if (i < npw) quant_pass(wv + kTileWaves * i, keep[i]);
+          after_pass(i);
         }
       }
       return;
@@ -428,14 +504,14 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
   }
 
   // ---- streaming passes (single-pass modes, or a second read of a large tile)
-  for (int p0 = 0; p0 < np; p0 += kLB) {
-    load_group(p0, true);
+  for (int i0 = 0; i0 < npw_max; i0 += kLB) {
+    load_group(i0, true);
     if constexpr (QM == LBFQ_Q_NONE) continue;
 #pragma unroll
     for (int i = 0; i < kLB; ++i) {
-      if (p0 + i < np) {
-        quant_pass(p0 + i, v[i], ok[i]);
-        after_pass(p0 + i);
+      if (i0 + i < npw_max) {
+        if (i0 + i < npw) quant_pass(wv + kTileWaves * (i0 + i), v[i]);
+        after_pass(i0 + i);
       }
     }
   }
@@ -536,6 +612,36 @@ __global__ void dequant_kernel(const uint8_t* codes, const float* scale, int64_t
 
 }  // namespace
 
+namespace {
+
+template <int DT, int QM>
+void launch_rowtile_qm(bool sub, bool had, dim3 grid, dim3 block, size_t shmem, hipStream_t st, const RowTileArgs& a) {
+  if constexpr (QM == LBFQ_Q_NONE || QM == LBFQ_Q_FP8_BLOCK || QM == LBFQ_Q_MX_QK) {
+    if (had) {
+      if (sub) hipLaunchKernelGGL((rowtile_kernel<DT, QM, true, true>), grid, block, shmem, st, a);
+      else hipLaunchKernelGGL((rowtile_kernel<DT, QM, false, true>), grid, block, shmem, st, a);
+      return;
+    }
+  }
+  if (sub) hipLaunchKernelGGL((rowtile_kernel<DT, QM, true, false>), grid, block, shmem, st, a);
+  else hipLaunchKernelGGL((rowtile_kernel<DT, QM, false, false>), grid, block, shmem, st, a);
+}
+
+template <int DT>
+void launch_rowtile(int qm, bool sub, bool had, dim3 grid, dim3 block, size_t shmem, hipStream_t st,
+                    const RowTileArgs& a) {
+  switch (qm) {
+    case LBFQ_Q_NONE: launch_rowtile_qm<DT, LBFQ_Q_NONE>(sub, had, grid, block, shmem, st, a); break;
+    case LBFQ_Q_FP8_BLOCK: launch_rowtile_qm<DT, LBFQ_Q_FP8_BLOCK>(sub, had, grid, block, shmem, st, a); break;
+    case LBFQ_Q_CHANNEL: launch_rowtile_qm<DT, LBFQ_Q_CHANNEL>(sub, had, grid, block, shmem, st, a); break;
+    case LBFQ_Q_MX_QK: launch_rowtile_qm<DT, LBFQ_Q_MX_QK>(sub, had, grid, block, shmem, st, a); break;
+    case LBFQ_Q_MX_V: launch_rowtile_qm<DT, LBFQ_Q_MX_V>(sub, had, grid, block, shmem, st, a); break;
+    default: launch_rowtile_qm<DT, LBFQ_Q_CHANNEL_AMAX>(sub, had, grid, block, shmem, st, a); break;
+  }
+}
+
+}  // namespace
+
 extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) {
   LBFQ_CHECK_ARG(p && p->x, "lbfq_rowtile: null input");
   LBFQ_CHECK_ARG(p->D == 64 || p->D == 128, "lbfq_rowtile: D must be 64 or 128; got %lld", (long long)p->D);
@@ -548,6 +654,8 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   const int qm = p->quant_mode;
   LBFQ_CHECK_ARG(qm >= LBFQ_Q_NONE && qm <= LBFQ_Q_CHANNEL_AMAX, "lbfq_rowtile: bad quant mode %d", qm);
   LBFQ_CHECK_ARG(qm == LBFQ_Q_NONE || qm == LBFQ_Q_CHANNEL_AMAX || p->codes, "lbfq_rowtile: missing codes");
+  LBFQ_CHECK_ARG(!p->hadamard || qm == LBFQ_Q_NONE || qm == LBFQ_Q_FP8_BLOCK || qm == LBFQ_Q_MX_QK,
+                 "lbfq_rowtile: the Hadamard rotation goes with quant modes NONE, FP8_BLOCK and MX_QK");
   LBFQ_CHECK_ARG(qm == LBFQ_Q_NONE || qm == LBFQ_Q_CHANNEL_AMAX || qm == LBFQ_Q_CHANNEL || p->scale,
                  "lbfq_rowtile: missing scale output");
   LBFQ_CHECK_ARG((qm != LBFQ_Q_CHANNEL && qm != LBFQ_Q_CHANNEL_AMAX) || p->amax_table,
@@ -558,6 +666,8 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   LBFQ_CHECK_ARG(qm != LBFQ_Q_MX_QK || (p->mx_block >= 8 && p->mx_block <= p->D && (p->mx_block & (p->mx_block - 1)) == 0),
                  "lbfq_rowtile: MX block along D must be a power of two in [8, D]; got %d", p->mx_block);
 
+  LBFQ_CHECK_ARG(p->S < (1ll << 31) && p->H * p->D < (1ll << 28) && p->codes_spitch < (1ll << 31),
+                 "lbfq_rowtile: S, H * D or the code pitch too large");
   LBFQ_CHECK_ARG(p->codes_layout != LBFQ_LAYOUT_BHDS || p->codes_spitch % 4 == 0,
                  "lbfq_rowtile: transposed codes pitch must be a multiple of 4");
   LBFQ_CHECK_ARG(p->codes_layout == LBFQ_LAYOUT_NHD || p->codes_spitch >= p->S, "lbfq_rowtile: bad codes pitch");
@@ -573,27 +683,18 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   a.scale_e8m0 = p->scale_e8m0;
   int64_t ntile = (p->S + p->R - 1) / p->R;
   const int64_t ntiles = p->B * p->H * ntile;
-  const int64_t nblocks = (ntiles + kTileWaves - 1) / kTileWaves;
+  a.ntile = static_cast<uint32_t>(ntile);
+  a.nsub = p->sub_mode == LBFQ_SUB_BLOCKVEC ? static_cast<uint32_t>(p->S / p->sub_block) : 0u;
+  const int64_t nblocks = ntiles;  // one workgroup per tile
   LBFQ_CHECK_ARG(nblocks < (1ll << 31), "lbfq_rowtile: grid too large");
   LBFQ_CHECK_ARG(p->R % (512 / p->D) == 0, "lbfq_rowtile: R must be a multiple of %lld", (long long)(512 / p->D));
-  size_t shmem = p->codes_layout == LBFQ_LAYOUT_BHDS ? static_cast<size_t>(kTileWaves * kStageRows * (p->D + 4)) : 0;
+  size_t shmem = p->codes_layout == LBFQ_LAYOUT_BHDS ? static_cast<size_t>(kStageRows * (p->D + 4)) : 0;
   const dim3 grid(static_cast<unsigned>(nblocks)), block(kTileWaves * 64);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-#define LBFQ_RT(DT, QM) hipLaunchKernelGGL((rowtile_kernel<DT, QM>), grid, block, shmem, st, a)
-#define LBFQ_RT_QM(DT)                                  \
-  switch (qm) {                                         \
-    case LBFQ_Q_NONE: LBFQ_RT(DT, LBFQ_Q_NONE); break;  \
-    case LBFQ_Q_FP8_BLOCK: LBFQ_RT(DT, LBFQ_Q_FP8_BLOCK); break; \
-    case LBFQ_Q_CHANNEL: LBFQ_RT(DT, LBFQ_Q_CHANNEL); break; \
-    case LBFQ_Q_MX_QK: LBFQ_RT(DT, LBFQ_Q_MX_QK); break; \
-    case LBFQ_Q_MX_V: LBFQ_RT(DT, LBFQ_Q_MX_V); break;  \
-    default: LBFQ_RT(DT, LBFQ_Q_CHANNEL_AMAX); break;   \
-  }
-  if (p->x_dtype == kBF16) { LBFQ_RT_QM(kBF16) }
-  else if (p->x_dtype == kF16) { LBFQ_RT_QM(kF16) }
-  else { LBFQ_RT_QM(kF32) }
-#undef LBFQ_RT_QM
-#undef LBFQ_RT
+  const bool sub = p->sub_mode != LBFQ_SUB_NONE, had = p->hadamard != 0;
+  if (p->x_dtype == kBF16) launch_rowtile<kBF16>(qm, sub, had, grid, block, shmem, st, a);
+  else if (p->x_dtype == kF16) launch_rowtile<kF16>(qm, sub, had, grid, block, shmem, st, a);
+  else launch_rowtile<kF32>(qm, sub, had, grid, block, shmem, st, a);
   LBFQ_LAUNCH_CHECK("lbfq_rowtile");
   return 0;
 }

@@ -131,3 +131,24 @@ def test_wan_padding_and_inputs():
     assert n == 1000 and qp.shape[1] == 1024
     assert torch.count_nonzero(qp[:, 1000:]) == 0
     assert torch.equal(kp[:, 1000:], ks[:, -1:].expand(1, 24, 2, 64))
+
+
+def test_rowtile_rejects_hadamard_with_v_modes():
+    """lbfq_rowtile applies the Hadamard rotation only with the Q/K quant modes
+    (NONE, FP8_BLOCK, MX_QK); with a V mode it returns an error before any
+    launch (host-side check, no GPU needed)."""
+    from low_bit_fake_quant import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    lib.lbfq_rowtile.argtypes = [ctypes.POINTER(_lib.RowTileParams), ctypes.c_void_p]
+    lib.lbfq_rowtile.restype = ctypes.c_int
+    lib.lbfq_last_error.restype = ctypes.c_char_p
+    for qm in (_lib.Q_CHANNEL, _lib.Q_MX_V, _lib.Q_CHANNEL_AMAX):
+        p = _lib.RowTileParams()
+        p.x = 0x1000; p.x_dtype = 2; p.B, p.S, p.H, p.D = 1, 256, 2, 128; p.R = 64
+        p.hadamard = 1; p.had_scale = 1.0; p.quant_mode = qm
+        p.codes = 0x2000; p.codes_layout = _lib.LAYOUT_BHDS; p.codes_spitch = 256
+        p.scale = 0x3000; p.amax_table = 0x4000; p.mx_block = 32
+        assert lib.lbfq_rowtile(ctypes.byref(p), None) != 0
+        assert b"Hadamard" in lib.lbfq_last_error()
