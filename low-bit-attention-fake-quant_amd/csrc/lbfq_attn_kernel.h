@@ -671,6 +671,21 @@ __device__ __forceinline__ void uta128_pack(const v16f (&s4)[4], const float (&f
 constexpr int attn_waves_per_simd(int bl, bool valpha, int bn) {
   return (bl == 3 || (bl != 0 && valpha) || (bn == 128 && bl != 0)) ? 1 : 2;
 }
+// V-smoothing correction acc[db][d, q] += valpha[d] * w (w: the lane's query)
+// as an outer product on the fp32 matrix cores: v_mfma_f32_32x32x2_f32 with
+// A[d][0] = valpha[32 db + d], B[0][q] = w and the K = 1 half (lanes 32-63)
+// zero.  Its output layout is the accumulator's, so it replaces 64 VALU FMAs
+// per lane (the kernel is VALU-issue-bound, the matrix cores are not).
+template <int NDB>
+__device__ __forceinline__ void valpha_outer(v16f (&acc)[NDB], const float* valpha, float w, int li, int g) {
+  const float bw = g == 0 ? w : 0.0f;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    const float av = g == 0 ? valpha[32 * db + li] : 0.0f;
+    acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bw, acc[db], 0, 0, 0);
+  }
+}
+
 template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA, int BN>
 __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN)) attn_fwd_kernel(const KArgs a) {
   static_assert(BN == 64 || BN == 128, "block_n is 64 or 128");
@@ -1316,17 +1331,7 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN))
 
     // ---- V smoothing: correction of tile it-1, in the units of its PV product
     // (added in this step), before this step's rescale ----------------------------
-    if constexpr (VALPHA) {
-      const float w = rsm[0] * vw_prev;
-      const VM& vmp = vmeta[vprev];
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = 32 * db + 8 * (r >> 2) + 4 * g + (r & 3);
-          acc[db][r] = fmaf(w, vmp.valpha[d], acc[db][r]);
-        }
-    }
+    if constexpr (VALPHA) valpha_outer<NDB>(acc, vmeta[vprev].valpha, rsm[0] * vw_prev, li, g);
 
     // ---- accumulator rescale for tile it (alpha, dynamic P scale, fp8_block V
     // scale): the PV of tile it, issued in the next step, accumulates on top ------
@@ -1412,14 +1417,7 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN))
     if constexpr (VALPHA) {  // correction of the last tile
       const v16f zero = {};
       const v16f rl = mfma32<false>(ones, pop_prev, zero, 0, 0);
-      const float w = rl[0] * vw_prev;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = 32 * db + 8 * (r >> 2) + 4 * g + (r & 3);
-          acc[db][r] = fmaf(w, vmeta[vl].valpha[d], acc[db][r]);
-        }
+      valpha_outer<NDB>(acc, vmeta[vl].valpha, rl[0] * vw_prev, li, g);
     }
   }
   } else {
@@ -1645,6 +1643,7 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN))
         const v16f zero = {};
         v16f rs = mfma32<false>(ones, popt[0], zero, 0, 0);
         rs = mfma32<false>(ones, popt[1], rs, 0, 0);
+        // (VALU FMAs here: the outer-product MFMAs take this step past 256 VGPRs)
         const float w = rs[0] * s_lp * rsig;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
