@@ -1348,21 +1348,9 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN))
     // an elided tile keeps sigma (f = 1: no rescale)
     const float sig_keep = elide ? sigma : sig_new;
     const float rsig = __builtin_amdgcn_rcpf(sig_keep);
-    if (elide && a.fill_kind != FILL_ZERO) {
-      const float w = __builtin_amdgcn_cvt_f32_fp8(fqw, 0) * s_lp * (v_blk ? vsc : 1.0f) * rsig;
-      const VM& vmc = vmeta[vcur];
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const float4 cs = *reinterpret_cast<const float4*>(&vmc.vcol[32 * db + 8 * r4 + 4 * g]);
-          acc[db][4 * r4 + 0] = fmaf(w, cs.x, acc[db][4 * r4 + 0]);
-          acc[db][4 * r4 + 1] = fmaf(w, cs.y, acc[db][4 * r4 + 1]);
-          acc[db][4 * r4 + 2] = fmaf(w, cs.z, acc[db][4 * r4 + 2]);
-          acc[db][4 * r4 + 3] = fmaf(w, cs.w, acc[db][4 * r4 + 3]);
-        }
-      }
-    }
+    if (elide && a.fill_kind != FILL_ZERO)
+      valpha_outer<NDB>(acc, vmeta[vcur].vcol, __builtin_amdgcn_cvt_f32_fp8(fqw, 0) * s_lp * (v_blk ? vsc : 1.0f) * rsig,
+                        li, g);
     const float f = elide ? 1.0f : alpha * sigma * rsig;
     sigma = sig_keep;
     if constexpr (VALPHA) vw_prev = s_lp * rsig;  // rowsum(P_deq) / sigma per code unit
