@@ -476,3 +476,22 @@ def test_batch_of_two_matches_oracle(gpu, name):
             continue
         one = fake_quant_attention(qi.to(gpu), ki.to(gpu), vi.to(gpu), cfg).cpu()
         assert torch.equal(one, out[i:i + 1]), f"{name}: batch entry {i} differs from its single run"
+
+
+@pytest.mark.parametrize("n", [1, 17, 63, 65, 129])
+@pytest.mark.parametrize("blasst", [False, True])
+def test_tiny_and_odd_sequence_lengths(gpu, n, blasst):
+    """S below one 64-key tile, one key past a tile, one tile past the
+    128-query workgroup: a single masked tile, the ring prefetch clamped to the
+    last tile, and a workgroup whose second wave holds no valid query.  MX Q/K
+    and channel V accept any S."""
+    from low_bit_fake_quant import fake_quant_attention
+    kw = dict(qk_quant="mxfp8", v_quant="fp8_channel", smoothing="k_only", q_kmeans_k=None,
+              p_quant="dynamic", rowmax_mode="online")
+    if blasst:
+        kw.update(blasst_lambda=0.05, blasst_fill="mean_a1.5")
+    cfg = _cfg(**kw)
+    q, k, v = _inputs(n=n, seed=40 + n, q_clusters=0)
+    out = fake_quant_attention(q.to(gpu), k.to(gpu), v.to(gpu), cfg).cpu()
+    assert out.shape == q.shape and torch.isfinite(out).all()
+    check_parity(out, q, k, v, cfg, f"S={n}{'/blasst' if blasst else ''}")
