@@ -668,8 +668,13 @@ __device__ __forceinline__ void uta128_pack(const v16f (&s4)[4], const float (&f
 // per SIMD).  BLASST together with V smoothing also runs one wave per SIMD.
 // BN: the reference's block_n, the keys that share one row-max update, one
 // P scale and one BLASST decision: 64 (one MFMA tile per step) or 128 (two).
-constexpr int attn_waves_per_simd(int bl, bool valpha, int bn) {
-  return (bl == 3 || (bl != 0 && valpha) || (bn == 128 && bl != 0)) ? 1 : 2;
+constexpr int attn_waves_per_simd(int d, int p_mode, int rb, int bl, bool valpha, int bn) {
+  if (bl == 3 || (bl != 0 && valpha)) return 1;
+  if (bn == 128 && bl == 2) return 1;
+  // block_n = 128 with a per-row fill fits 256 VGPRs, except the online-row-max
+  // variants with a scaled P at D = 128
+  if (bn == 128 && bl == 1 && d == 128 && p_mode != 0 && rb == 0) return 1;
+  return 2;
 }
 // V-smoothing correction acc[db][d, q] += valpha[d] * w (w: the lane's query)
 // as an outer product on the fp32 matrix cores: v_mfma_f32_32x32x2_f32 with
@@ -687,7 +692,7 @@ __device__ __forceinline__ void valpha_outer(v16f (&acc)[NDB], const float* valp
 }
 
 template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA, int BN>
-__global__ void __launch_bounds__(kThreads, attn_waves_per_simd(BL, VALPHA, BN)) attn_fwd_kernel(const KArgs a) {
+__global__ void __launch_bounds__(kThreads, attn_waves_per_simd(D, P_MODE, RB, BL, VALPHA, BN)) attn_fwd_kernel(const KArgs a) {
   static_assert(BN == 64 || BN == 128, "block_n is 64 or 128");
   constexpr bool BLASST = BL != 0;
   // BLASST with one fill value per row and tile, without V smoothing: a tile
