@@ -61,24 +61,6 @@ struct RowTileArgs {
   uint32_t nsub;   // S / sub_block (BLOCKVEC)
 };
 
-__device__ __forceinline__ void load8(const void* x, int dt, int64_t idx, float v[8]) {
-  if (dt == kF32) {
-    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + idx);
-    float4 a = p[0], b = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + idx);
-    uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint16_t lo = static_cast<uint16_t>(w[i] & 0xffffu), hi = static_cast<uint16_t>(w[i] >> 16);
-      if (dt == kBF16) { v[2 * i] = bf16_bits_to_f32(lo); v[2 * i + 1] = bf16_bits_to_f32(hi); }
-      else { v[2 * i] = f16_bits_to_f32(lo); v[2 * i + 1] = f16_bits_to_f32(hi); }
-    }
-  }
-}
-
 __device__ __forceinline__ void store8(void* y, int dt, int64_t idx, const float v[8]) {
   if (dt == kF32) {
     float4* p = reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + idx);
@@ -159,7 +141,7 @@ __device__ __forceinline__ float round_dt(float v) {
 // is read twice.  Transposed (BHDS) codes go through an LDS stage of
 // kStageRows rows that all 256 threads write out as dwords of four
 // consecutive keys.  Consecutive workgroups take adjacent heads of one row
-// tile (adjacent 16-byte pieces of the same rows).  SUB (a mean is
+// tile (adjacent D-element pieces of the same NHD rows).  SUB (a mean is
 // subtracted) and HAD (FWHT) are compile-time so that the common cases carry
 // no per-element work for the others; the kernel is VALU-issue-bound.
 constexpr int kTileWaves = 4;
