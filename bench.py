@@ -40,6 +40,7 @@ import torch  # noqa: E402
 
 FP8_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 MFMA (datasheet)
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+FP32_PEAK_TFLOPS = 157.3   # MI355X fp32 (vector / MFMA, dense)
 
 
 def log(msg: str) -> None:
@@ -315,6 +316,23 @@ def main() -> int:
                "preprocess_ms": prep_ms, "algorithmic_bytes": quant_bytes,
                "note": "quantisers + qm.K_s table; algorithmic bytes (inputs read once, outputs written once) / time"}
     prepass["frac_of_hbm_peak"] = prepass["quantise_qmk_GBps"] / HBM_PEAK_GBS
+    if cfg.q_kmeans_k is not None:
+        # Q k-means alone (part of the uncached preprocess): `iters` assignment
+        # passes (2 S K D flops per head each, fp32 VALU in a fixed order) and
+        # iters - 1 centroid updates, each pass reading Q once
+        from low_bit_fake_quant._ops import kmeans
+        kk, it = cfg.q_kmeans_k, cfg.q_kmeans_iters
+        km_ms = _events_time(lambda: kmeans(qd, kk, it, cfg.q_kmeans_seed), 3, 1)
+        km_flops = it * 2.0 * s * kk * d * h * b
+        km_bytes = (2 * it - 1) * elem * qd.element_size()
+        prepass["kmeans"] = {"k": kk, "iters": it, "ms": km_ms,
+                             "assign_TFLOPs": km_flops / (km_ms * 1e-3) / 1e12,
+                             "frac_of_fp32_peak": km_flops / (km_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
+                             "GBps": km_bytes / (km_ms * 1e-3) / 1e9,
+                             "note": "assignment flops (2 S K D per head and pass) against the fp32 peak; "
+                                     "bytes = Q read once per pass"}
+        log(f"k-means: {km_ms:.3f} ms ({prepass['kmeans']['assign_TFLOPs']:.1f} TFLOP/s assign, "
+            f"{prepass['kmeans']['GBps']:.0f} GB/s)")
 
     cpu_baseline = None
     err = err_replay = None

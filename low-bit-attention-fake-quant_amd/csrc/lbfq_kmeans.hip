@@ -96,7 +96,32 @@ __global__ void __launch_bounds__(256) km_assign_kernel(const void* x, int64_t S
   load_row<DT>(x, ((b * S + t) * H + h) * D, xv);
   float best = INFINITY;
   int bj = 0;
-  for (int j = 0; j < K; ++j) {
+  // two centroids at a time: independent dot-product chains (each still
+  // sequential in d), compared in centroid order, so the first minimum wins
+  constexpr int KJ = 2;
+  int j = 0;
+  for (; j + KJ <= K; j += KJ) {
+    float dot[KJ];
+#pragma unroll
+    for (int u = 0; u < KJ; ++u) dot[u] = 0.0f;
+#pragma unroll
+    for (int d4 = 0; d4 < D / 4; ++d4) {
+#pragma unroll
+      for (int u = 0; u < KJ; ++u) {
+        const float4 cv = c_lds[(j + u) * (D / 4) + d4];
+        dot[u] = fmaf(xv[4 * d4], cv.x, dot[u]);
+        dot[u] = fmaf(xv[4 * d4 + 1], cv.y, dot[u]);
+        dot[u] = fmaf(xv[4 * d4 + 2], cv.z, dot[u]);
+        dot[u] = fmaf(xv[4 * d4 + 3], cv.w, dot[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < KJ; ++u) {
+      const float sc = fmaf(-2.0f, dot[u], cn_lds[j + u]);
+      if (sc < best) { best = sc; bj = j + u; }
+    }
+  }
+  for (; j < K; ++j) {
     const float4* c = c_lds + j * (D / 4);
     float dot = 0.0f;
 #pragma unroll
