@@ -316,6 +316,18 @@ def main() -> int:
                "preprocess_ms": prep_ms, "algorithmic_bytes": quant_bytes,
                "note": "quantisers + qm.K_s table; algorithmic bytes (inputs read once, outputs written once) / time"}
     prepass["frac_of_hbm_peak"] = prepass["quantise_qmk_GBps"] / HBM_PEAK_GBS
+    # the practical ceiling, measured in the same run: a 1 GiB device copy
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    copy_ms = _events_time(lambda: dst.copy_(src), 5, 2)
+    del src, dst
+    copy_gbs = 2 * (1 << 30) / (copy_ms * 1e-3) / 1e9
+    prepass["copy_GBps"] = copy_gbs
+    prepass["frac_of_copy_rate"] = prepass["quantise_qmk_GBps"] / copy_gbs
+    # on the reference's own bytes: Q/K/V read, codes written, no correction table
+    ref_bytes = 3 * elem * 2 + 3 * elem * 1
+    prepass["reference_bytes"] = ref_bytes
+    prepass["reference_bytes_GBps"] = ref_bytes / (quant_ms * 1e-3) / 1e9
     if cfg.q_kmeans_k is not None:
         # Q k-means alone (part of the uncached preprocess): `iters` assignment
         # passes (2 S K D flops per head each, fp32 VALU in a fixed order) and
