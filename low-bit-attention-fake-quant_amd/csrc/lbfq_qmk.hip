@@ -188,14 +188,16 @@ __device__ __forceinline__ float half_max16(float (&x)[16], int li) {
 
 // qm rows split into three bf16 pieces hi + mid + lo (qm to 24 bits), once per
 // (b, h, group): out[((b*H + h)*3 + piece)*G + g][dp] holds the bf16 pair of
-// dimensions 2 dp, 2 dp + 1 (low half = even dimension).
+// dimensions 2 dp, 2 dp + 1 (low half = even dimension).  With rowmax_bits,
+// the same launch sets the row-max accumulators (B*H*G, ordered bits) to -inf.
 template <int D>
 __global__ void __launch_bounds__(256) qm_split_kernel(const float* qm, int64_t B, int64_t H, int64_t G,
-                                                       uint32_t* out) {
+                                                       uint32_t* out, uint32_t* rowmax_bits) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // over B*H*G*(D/2)
   if (i >= B * H * G * (D / 2)) return;
   const int dp = static_cast<int>(i % (D / 2));
   const int64_t r = i / (D / 2);
+  if (rowmax_bits && dp == 0) rowmax_bits[r] = ordered_bits(-INFINITY);  // r = (b*H + h)*G + g
   const int64_t g = r % G, bh = r / G;
   const int64_t b = bh / H, h = bh % H;
   const float2 x = *reinterpret_cast<const float2*>(qm + ((b * G + g) * H + h) * D + 2 * dp);
@@ -461,10 +463,6 @@ int qmk_launch(const float* qm, const void* ks, int ks_dtype, const int32_t* gat
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint32_t* rb = reinterpret_cast<uint32_t*>(rowmax);
   const int64_t nr = B * H * G;
-  if (rb) {
-    hipLaunchKernelGGL(fill_ordered_kernel, dim3(static_cast<unsigned>((nr + 255) / 256)), dim3(256), 0, st, rb, nr);
-    LBFQ_LAUNCH_CHECK("lbfq_qmk fill");
-  }
   // bf16 K: the bf16 matrix-core kernel (its table offsets within one head are 32-bit)
   if (ks_dtype == kBF16 && (!bias || G * s_pitch * 4 < (int64_t{1} << 32))) {
     LBFQ_CHECK_ARG(qm_split, "lbfq_qmk: bf16 K needs the qm_split workspace (B*H*3*G*D/2 words)");
@@ -475,12 +473,12 @@ int qmk_launch(const float* qm, const void* ks, int ks_dtype, const int32_t* gat
     const int64_t ns = B * H * G * (D / 2);
     const dim3 gs(static_cast<unsigned>((ns + 255) / 256));
     if (D == 128) {
-      hipLaunchKernelGGL(qm_split_kernel<128>, gs, dim3(256), 0, st, qm, B, H, G, qm_split);
+      hipLaunchKernelGGL(qm_split_kernel<128>, gs, dim3(256), 0, st, qm, B, H, G, qm_split, rb);
       hipLaunchKernelGGL(qmk_bf16_kernel<128>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm_split, k16,
                          gather, ks_mean, B, S, H, G, scale, bias, s_pitch, rb, k_codes, k_scale, k_pitch,
                          static_cast<int>(k_block));
     } else {
-      hipLaunchKernelGGL(qm_split_kernel<64>, gs, dim3(256), 0, st, qm, B, H, G, qm_split);
+      hipLaunchKernelGGL(qm_split_kernel<64>, gs, dim3(256), 0, st, qm, B, H, G, qm_split, rb);
       hipLaunchKernelGGL(qmk_bf16_kernel<64>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st, qm_split, k16,
                          gather, ks_mean, B, S, H, G, scale, bias, s_pitch, rb, k_codes, k_scale, k_pitch,
                          static_cast<int>(k_block));
@@ -493,6 +491,10 @@ int qmk_launch(const float* qm, const void* ks, int ks_dtype, const int32_t* gat
     return 0;
   }
   LBFQ_CHECK_ARG(!k_codes, "lbfq_qmk_kquant: the fused K quantiser needs bf16 K and a table under 4 GiB per head");
+  if (rb) {
+    hipLaunchKernelGGL(fill_ordered_kernel, dim3(static_cast<unsigned>((nr + 255) / 256)), dim3(256), 0, st, rb, nr);
+    LBFQ_LAUNCH_CHECK("lbfq_qmk fill");
+  }
   const int64_t nblk = B * H * ((S + kKeysPerBlock - 1) / kKeysPerBlock);
   LBFQ_CHECK_ARG(nblk < (int64_t{1} << 31), "lbfq_qmk: grid too large");
   if (D == 128)
