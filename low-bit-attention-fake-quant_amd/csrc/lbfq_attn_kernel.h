@@ -1382,8 +1382,9 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(D, P_MODE, RB, B
     // instead of being copied at the back edge.  Kernels that carry more
     // state through a step -- V smoothing, the packed UTA fill codes, the
     // per-row fills with MX Q/K -- need more than the 256 VGPRs of two waves
-    // per SIMD when unrolled and spill inside the loop, so they run one step
-    // per iteration (ring slots then come from it % 4).
+    // per SIMD when unrolled four times and spill inside the loop, so they run
+    // two steps per iteration (ring slots then come from it % 4; the packed
+    // UTA fills spill even at two and run one).
     constexpr bool UNROLL = !VALPHA && (BL == 0 || BL == 3 || (BL == 1 && !QK_MX));
     int it0 = 0;
     if constexpr (UNROLL) {
@@ -1392,6 +1393,12 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(D, P_MODE, RB, B
         step(it0 + 1, std::false_type{}, 1);
         step(it0 + 2, std::false_type{}, 2);
         step(it0 + 3, std::false_type{}, 3);
+      }
+    }
+    if constexpr (!UNROLL && BL != 2) {
+      for (; it0 + 1 < nfull; it0 += 2) {
+        step(it0, std::false_type{}, it0 & 3);
+        step(it0 + 1, std::false_type{}, (it0 + 1) & 3);
       }
     }
     for (; it0 < nfull; ++it0) step(it0, std::false_type{}, it0 & 3);
