@@ -234,7 +234,7 @@ def main() -> int:
     torch.cuda.synchronize()
     prep_ms = _events_time(lambda: _lazy_preprocess(qd, kd, vd, cfg), 3, 1)
     prep = _lazy_preprocess(qd, kd, vd, cfg)
-    quant_ms = _events_time(lambda: quantize_operands(prep, cfg, sm_scale), 5, 2)
+    quant_ms = _events_time(lambda: quantize_operands(prep, cfg, sm_scale), 20, 3)
     ops = quantize_operands(prep, cfg, sm_scale)
     torch.cuda.synchronize()
     log(f"prepass: preprocess {prep_ms:.3f} ms, quantise+qmk {quant_ms:.3f} ms")
