@@ -192,6 +192,59 @@ def traffic_from_profile(config: int):
     return None
 
 
+def clock_sample(ops, cfg, sm_scale, launches, flops, launch_attention) -> int:
+    """Shader clock under a long run of the attention kernel: rocm-smi is
+    sampled from a thread while `launches` launches run back to back.  The
+    datasheet FP8 peak (5.0 PFLOP/s) is quoted at 2.4 GHz; the rate is also
+    reported against that peak scaled to the median sampled clock."""
+    import re
+    import subprocess
+    import threading
+
+    def sclk_mhz():
+        r = subprocess.run(["rocm-smi", "--showclocks", "--csv"], capture_output=True, text=True, timeout=10)
+        m = re.search(r"card0,\((\d+)Mhz\),\d+,\((\d+)Mhz\)", r.stdout)
+        return (int(m.group(2)), int(m.group(1))) if m else None
+
+    launch_attention(ops, cfg, sm_scale, torch.bfloat16)
+    torch.cuda.synchronize()
+    idle = sclk_mhz()
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        t0 = time.time()
+        while not stop.is_set():
+            c = sclk_mhz()
+            if c:
+                samples.append((time.time() - t0, c[0], c[1]))
+            time.sleep(0.25)
+
+    th = threading.Thread(target=sampler)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    th.start()
+    e0.record()
+    for _ in range(launches):
+        launch_attention(ops, cfg, sm_scale, torch.bfloat16)
+    e1.record()
+    torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    ms = e0.elapsed_time(e1) / launches
+    busy = [c for t, c, _ in samples[2:-2]] or [c for _, c, _ in samples]
+    busy.sort()
+    med = busy[len(busy) // 2] if busy else float("nan")
+    tflops = flops / (ms * 1e-3) / 1e12
+    peak_at_clk = FP8_PEAK_TFLOPS * med / 2400.0
+    for t, c, mc in samples:
+        log(f"t={t:5.2f}s sclk {c} MHz mclk {mc} MHz")
+    print(json.dumps({"launches": launches, "ms_per_launch": ms, "TFLOPs": tflops,
+                      "sclk_idle_MHz": idle[0] if idle else None, "sclk_median_MHz": med,
+                      "sclk_samples": len(samples), "frac_of_fp8_peak_2400MHz": tflops / FP8_PEAK_TFLOPS,
+                      "fp8_peak_at_median_clock_TFLOPs": peak_at_clk,
+                      "frac_of_clock_scaled_peak": tflops / peak_at_clk}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,6 +258,9 @@ def main() -> int:
                     help="skip timing configs 1, 3 and 4 beside the headline config")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="driver for rocprofv3 --pmc passes: a 1 GiB calibration copy, then one attention launch")
+    ap.add_argument("--clock-sample", type=int, default=0, metavar="LAUNCHES",
+                    help="run LAUNCHES attention launches back to back while sampling the shader clock with "
+                         "rocm-smi; print the samples and the rate against the clock-scaled FP8 peak")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU per process; --gpus N>1 is not supported "
@@ -251,6 +307,9 @@ def main() -> int:
         torch.cuda.synchronize()
         log("pmc pass: calibration copy + one attention launch done")
         return 0
+
+    if args.clock_sample:
+        return clock_sample(ops, cfg, sm_scale, args.clock_sample, attention_flops(n_real, h, d, b), launch_attention)
 
     # ---- attention kernel: the timed step ----------------------------------
     out = launch_attention(ops, cfg, sm_scale, torch.bfloat16)
