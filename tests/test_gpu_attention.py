@@ -345,13 +345,13 @@ def test_reference_gap_comes_from_the_scores(gpu, name):
     assert max_abs(r32, ref) > MAXABS
 
 
-@pytest.mark.parametrize("config", [2, 4])
+@pytest.mark.parametrize("config", [1, 2, 3, 4])
 def test_full_length_padded_wan_shapes(gpu, config):
-    """BASELINE configs 2 and 4 at their real lengths (N = 32760 and 75600,
-    padded per the Wan hook: Q zero rows, K/V repeat the last row,
+    """BASELINE configs 1-4 at their real lengths (N = 32760, and 75600 for
+    config 4, padded per the Wan hook: Q zero rows, K/V repeat the last row,
     bench/wan_attention_hook.py:249-294), 2 heads, 256 rows of the padded
-    problem checked against the replay (strict), the reference (cosine,
-    config 2) and, for BLASST, the per-row skip counts (exact)."""
+    problem checked against the replay (strict), the reference (cosine, the
+    dense configurations) and, for BLASST, the per-row skip counts (exact)."""
     from low_bit_fake_quant.attention_kernel import launch_attention
     from low_bit_fake_quant.wan import make_inputs, pad_qkv, workloads
     w = workloads()[config]
