@@ -202,7 +202,10 @@ def clock_sample(ops, cfg, sm_scale, launches, flops, launch_attention) -> int:
     import threading
 
     def sclk_mhz():
-        r = subprocess.run(["rocm-smi", "--showclocks", "--csv"], capture_output=True, text=True, timeout=10)
+        try:
+            r = subprocess.run(["rocm-smi", "--showclocks", "--csv"], capture_output=True, text=True, timeout=10)
+        except (OSError, subprocess.SubprocessError):
+            return None
         m = re.search(r"card0,\((\d+)Mhz\),\d+,\((\d+)Mhz\)", r.stdout)
         return (int(m.group(2)), int(m.group(1))) if m else None
 
