@@ -316,31 +316,56 @@ __global__ void __launch_bounds__(256) qmk_bf16_kernel(const uint32_t* qsplit, c
   u32x4 kb[kBfKeyBlocks][NKS];
   bool nvalid[kBfKeyBlocks];
 #pragma unroll
-  for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
-    const int64_t n = nw0 + 32 * kbi + li;
-    nvalid[kbi] = n < S;
-    const int64_t src = nvalid[kbi] ? (gather ? gather[bh * S + n] : n) : 0;
-    const uint16_t* row = ks + ((b * S + src) * H + h) * D;
+  for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) nvalid[kbi] = nw0 + 32 * kbi + li < S;
+  // Smoothed rows -> B operands.  The rows are read coalesced (16 lanes per
+  // 256-byte row, 4 rows per instruction) into a per-wave LDS staging area
+  // (the qm chunk buffers, not yet in use), one 32-key block at a time, and
+  // read back in the MFMA layout: lane (li, hf) takes dimensions
+  // 16 st + 8 hf + [0, 8) of key li.  16-byte chunk c of row r sits at chunk
+  // slot c ^ (r & 15), so both the row writes and the column reads spread
+  // over the LDS banks.
+  {
+    uint8_t* stg = reinterpret_cast<uint8_t*>(&qs[0][0][0][0]) + wave * (32 * D * 2);
+    constexpr int CPR = D / 8;          // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;       // rows per load instruction
+    const int cl = lane % CPR, rl = lane / CPR;
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) {
-      const int d0 = 16 * st + 8 * hf;
-      const uint4 r = *reinterpret_cast<const uint4*>(row + d0);
-      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-      float x[8];
+    for (int kbi = 0; kbi < kBfKeyBlocks; ++kbi) {
+      uint4 raw[32 / RPI];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
-        x[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+      for (int j = 0; j < 32 / RPI; ++j) {
+        const int r = rl + RPI * j;
+        const int64_t n = nw0 + 32 * kbi + r;
+        const int64_t src = n < S ? (gather ? gather[bh * S + n] : n) : 0;
+        raw[j] = *reinterpret_cast<const uint4*>(ks + ((b * S + src) * H + h) * D + 8 * cl);
       }
-      if (mean) {
-        const float4 m0 = *reinterpret_cast<const float4*>(mean + bh * D + d0);
-        const float4 m1 = *reinterpret_cast<const float4*>(mean + bh * D + d0 + 4);
-        const float mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] -= mm[i];  // rounded to bf16 by the packing
+      for (int j = 0; j < 32 / RPI; ++j) {
+        const int r = rl + RPI * j;
+        *reinterpret_cast<uint4*>(stg + r * (D * 2) + 16 * (cl ^ (r & (CPR - 1)))) = raw[j];
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kb[kbi][st][i] = nvalid[kbi] ? pack_bf16(x[2 * i], x[2 * i + 1]) : 0u;
+      for (int st = 0; st < NKS; ++st) {
+        const int d0 = 16 * st + 8 * hf;
+        const int c = 2 * st + hf;
+        const uint4 r = *reinterpret_cast<const uint4*>(stg + li * (D * 2) + 16 * (c ^ (li & (CPR - 1))));
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[2 * i] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+          x[2 * i + 1] = bf16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+        }
+        if (mean) {
+          const float4 m0 = *reinterpret_cast<const float4*>(mean + bh * D + d0);
+          const float4 m1 = *reinterpret_cast<const float4*>(mean + bh * D + d0 + 4);
+          const float mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] -= mm[i];  // rounded to bf16 by the packing
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kb[kbi][st][i] = nvalid[kbi] ? pack_bf16(x[2 * i], x[2 * i + 1]) : 0u;
+      }
     }
   }
   if (kcodes) kquant_wave<D>(kb, nvalid, bh, nw0, li, hf, S, kcodes, kscale, kpitch, kblk);
@@ -361,6 +386,7 @@ __global__ void __launch_bounds__(256) qmk_bf16_kernel(const uint32_t* qsplit, c
   const bool keys_full = nw0 + KPW <= S;  // wave-uniform
   const uint32_t sp = static_cast<uint32_t>(s_pitch);
   qm_chunk_load<D>(qv, qh, 0, Gi, tid);
+  __syncthreads();  // every wave has read its K rows out of the staging area
   qm_chunk_stage<D>(qv, &qs[0][0][0][0], tid);
   __syncthreads();
   qm_chunk_load<D>(qv, qh, 32, Gi, tid);  // rows are clamped to G - 1, so these loads are always in bounds
