@@ -75,6 +75,10 @@ typedef struct {
   int mx_block;                            /* MX-QK columns per scale (8..D)    */
   int smoothed_stage;                      /* 0: after subtract, 1: after FWHT  */
   int scale_e8m0;                          /* MX modes: write E8M0 bytes, not fp32 */
+  int64_t h_begin, h_count;                /* heads [h_begin, h_begin + h_count) of */
+                                           /* the H (h_count 0: all), so a head     */
+                                           /* chunk can be processed by a pass pair */
+                                           /* while its input is still cached       */
 } lbfq_rowtile_params;
 
 int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream);
@@ -190,9 +194,10 @@ typedef struct {
                                   /* row skipped (the per-row decisions behind the  */
                                   /* stats, attention_triton.py:165-175), or NULL   */
   int32_t* blasst_wave_tiles;     /* (B*H, ceil(S/128)*4, 2) int32, or NULL: per    */
-                                  /* wave of 32 reordered query rows, the 64-key    */
-                                  /* tiles every row of it skipped and the tiles    */
-                                  /* some row of it skipped                         */
+                                  /* wave of 32 reordered query rows, the block_n-  */
+                                  /* key decision blocks (64-key tiles at block_n   */
+                                  /* 64, 128-key blocks at 128) every row of it     */
+                                  /* skipped and those some row of it skipped       */
   const float* v_tile_colsum;     /* (B*H, s_pitch/64, D) from lbfq_v_tile_colsum, */
                                   /* or NULL.  With a per-row BLASST fill (not uta) */
                                   /* and no V smoothing, a full tile that all 32    */
@@ -312,6 +317,16 @@ typedef struct {
 } lbfq_blasst_attend_params;
 
 int lbfq_blasst_attend(const lbfq_blasst_attend_params* p, lbfq_stream_t stream);
+
+/* ---- measurement probe ----------------------------------------------------- */
+/* HBM streaming probe (no counterpart in the reference: it measures the
+ * ceiling the prepass is held against).  mode 0 reads `bytes` from src
+ * (global_load_dwordx4; sink: 256 uint32 that receive nothing in practice),
+ * 1 writes them to dst, 2 copies src to dst; `grid` workgroups of 256
+ * threads walk 16 KiB chunks grid-stride.  bytes % 16 == 0, 16-byte aligned
+ * pointers. */
+int lbfq_hbm_stream(int mode, const void* src, void* dst, int64_t bytes, int grid, uint32_t* sink,
+                    lbfq_stream_t stream);
 
 /* ---- building-block self tests (GPU unit tests of compiler builtins) ------ */
 /* E4M3 conversion of n fp32 values (n even) by the hardware converter. */

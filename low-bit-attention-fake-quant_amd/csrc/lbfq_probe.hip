@@ -6,6 +6,9 @@
 //   FA4-style online rule or the qm_k estimate with up/down thresholds (the
 //   reference diagnostic bench/count_rowmax_updates_triton.py:27-171), over
 //   the FP8 codes and qm correction table the attention kernel consumes.
+// * hbm_stream: read-only / write-only / copy streams of 16-byte words, the
+//   measured HBM ceiling the prepass is held against (no reference
+//   counterpart).
 #include "lbfq_common.h"
 #include "../../include/lbfq.h"
 
@@ -221,7 +224,79 @@ __global__ void __launch_bounds__(256) rowmax_count_kernel(const CountArgs a) {
   }
 }
 
+// HBM streaming probe: 256 threads, each moving kUnroll 16-byte words per
+// chunk of 256 * kUnroll words (a wave touches 1 KiB contiguous per load);
+// chunks are dealt out grid-stride.  MODE 0 reads and folds the words into
+// one value per thread, stored only when it equals a constant (so the loads
+// are live but nothing is written); MODE 1 writes; MODE 2 copies.
+constexpr int kStreamThreads = 256;
+constexpr int kStreamUnroll = 4;
+
+template <int MODE>
+__global__ void __launch_bounds__(kStreamThreads) hbm_stream_kernel(const uint4* __restrict__ src,
+                                                                    uint4* __restrict__ dst, int64_t n16,
+                                                                    uint32_t* sink) {
+  constexpr int64_t kChunk = kStreamThreads * kStreamUnroll;
+  const int64_t nchunk = (n16 + kChunk - 1) / kChunk;
+  uint32_t acc = 0;
+  for (int64_t c = blockIdx.x; c < nchunk; c += gridDim.x) {
+    const int64_t base = c * kChunk + threadIdx.x;
+    uint4 v[kStreamUnroll];
+    if (base + kStreamThreads * (kStreamUnroll - 1) < n16) {
+      if constexpr (MODE != 1) {
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) v[u] = src[base + kStreamThreads * u];
+      }
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const int64_t i = base + kStreamThreads * u;
+        if constexpr (MODE == 0) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        if constexpr (MODE == 1) dst[i] = make_uint4(static_cast<uint32_t>(i), 0u, 0u, 0u);
+        if constexpr (MODE == 2) dst[i] = v[u];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const int64_t i = base + kStreamThreads * u;
+        if (i < n16) {
+          if constexpr (MODE == 0) {
+            const uint4 w = src[i];
+            acc ^= w.x ^ w.y ^ w.z ^ w.w;
+          }
+          if constexpr (MODE == 1) dst[i] = make_uint4(static_cast<uint32_t>(i), 0u, 0u, 0u);
+          if constexpr (MODE == 2) dst[i] = src[i];
+        }
+      }
+    }
+  }
+  if constexpr (MODE == 0) {
+    if (acc == 0x9e3779b9u) sink[threadIdx.x] = acc;
+  }
+}
+
 }  // namespace
+
+extern "C" int lbfq_hbm_stream(int mode, const void* src, void* dst, int64_t bytes, int grid, uint32_t* sink,
+                               lbfq_stream_t stream) {
+  LBFQ_CHECK_ARG(mode >= 0 && mode <= 2, "lbfq_hbm_stream: mode must be 0 (read), 1 (write) or 2 (copy)");
+  LBFQ_CHECK_ARG(bytes > 0 && bytes % 16 == 0, "lbfq_hbm_stream: bytes must be a positive multiple of 16");
+  LBFQ_CHECK_ARG(grid > 0, "lbfq_hbm_stream: grid must be > 0");
+  LBFQ_CHECK_ARG(mode == 1 || (src && reinterpret_cast<uintptr_t>(src) % 16 == 0),
+                 "lbfq_hbm_stream: src must be 16-byte aligned");
+  LBFQ_CHECK_ARG(mode == 0 || (dst && reinterpret_cast<uintptr_t>(dst) % 16 == 0),
+                 "lbfq_hbm_stream: dst must be 16-byte aligned");
+  LBFQ_CHECK_ARG(mode != 0 || sink, "lbfq_hbm_stream: mode 0 needs a sink of 256 words");
+  const int64_t n16 = bytes / 16;
+  const dim3 g(static_cast<unsigned>(grid)), blk(kStreamThreads);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint4* s4 = static_cast<const uint4*>(src);
+  uint4* d4 = static_cast<uint4*>(dst);
+  if (mode == 0) hipLaunchKernelGGL(hbm_stream_kernel<0>, g, blk, 0, st, s4, d4, n16, sink);
+  else if (mode == 1) hipLaunchKernelGGL(hbm_stream_kernel<1>, g, blk, 0, st, s4, d4, n16, sink);
+  else hipLaunchKernelGGL(hbm_stream_kernel<2>, g, blk, 0, st, s4, d4, n16, sink);
+  LBFQ_LAUNCH_CHECK("lbfq_hbm_stream");
+  return 0;
+}
 
 extern "C" int lbfq_p_requant_rows(const void* scores, int dtype, int64_t B, int64_t M, int64_t N, int64_t ssb,
                                    int64_t ssm, int64_t ssn, uint8_t* p, int64_t psb, int64_t psm, int64_t psn,

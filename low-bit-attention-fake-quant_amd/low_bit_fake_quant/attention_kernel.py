@@ -201,7 +201,8 @@ def launch_attention(ops, cfg, sm_scale: float, out_dtype: torch.dtype, *, retur
     """Run the attention kernel on quantised operands; returns NHD output, then
     (when asked) the BLASST stats (ceil(S/block_m), B*H, 2), the per-row
     skipped K-block counts (B*H, S) in output-row order, and per wave of 32
-    reordered query rows the number of 64-key tiles that every row of the wave
+    reordered query rows the number of block_n-key decision blocks (64-key
+    tiles at block_n = 64, 128-key blocks at 128) that every row of the wave
     skipped (softmax and PV elided) and that some row skipped,
     (B*H, ceil(S/128)*4, 2) int32.  ``rowmax_init`` (B*H, S) fp32: the
     initial row max of each (reordered) query row in log2 units

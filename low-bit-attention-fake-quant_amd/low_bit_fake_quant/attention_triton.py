@@ -12,12 +12,14 @@ into codes:
   ``block_m``, 128, 64, 32, 16 rows whose re-quantisation reproduces the
   input exactly (dequantised fp8_block values come back as the same codes);
   when none does (values that were never FP8), 16-row blocks are used and
-  the result carries that FP8 rounding.
+  the result carries that FP8 rounding (a ``RequantWarning`` says so; the
+  reference runs bf16 dots on those values).
 * V (``v_bhsd_bf16``): the E4M3 codes of its values when they all are E4M3
   values (the "FP8-cast bf16" input of the reference), with ``v_scale_bhd``
   as the per-channel scale or ``v_block_scale_bsh`` as the fp8_block scale;
   otherwise (pre-dequantised bf16 with unit scales) per-channel FP8 codes
-  whose scales multiply ``v_scale_bhd``.
+  whose scales multiply ``v_scale_bhd`` (with a ``RequantWarning``: the
+  reference multiplies the bf16 values themselves).
 * The qm correction (``qm_bhgd`` with ``k_smooth_bhsd``) becomes the
   kernel's per-group table; ``rowmax_est_bhs`` must be constant within each
   q_smooth_block group (the kernel holds one estimate per group, as the qm_k
@@ -28,6 +30,8 @@ Limits of the gfx950 kernel: block_n in {64, 128}; D in {64, 128}.
 
 from __future__ import annotations
 
+import warnings
+
 import torch
 
 from ._ops import RowSource, qmk
@@ -37,6 +41,12 @@ from .config import QuantConfig
 from .quant import fp8_block_dequant, fp8_block_quant, fp8_per_channel_quant
 
 LOG2E = 1.4426950408889634
+
+
+class RequantWarning(UserWarning):
+    """The kernel-level entry re-quantised an input that was not FP8-valued:
+    the gfx950 kernel multiplies FP8 codes, so the result carries an FP8
+    rounding of that input which the reference (bf16 dots) does not apply."""
 
 
 def _requant_qk(x_bhsd: torch.Tensor, block_m: int, P: int):
@@ -67,20 +77,20 @@ def _requant_qk(x_bhsd: torch.Tensor, block_m: int, P: int):
 
 def _v_codes(v_bhsd: torch.Tensor, v_scale_bhd: torch.Tensor, P: int, block_scale):
     """V^T codes (B,H,D,P) and the kernel's V scale tensor; returns
-    (codes_t, scale, v_kind)."""
+    (codes_t, scale, v_kind, exact) -- exact: V was E4M3-valued."""
     b, h, s, d = v_bhsd.shape
     codes_t = (torch.zeros if P > s else torch.empty)((b, h, d, P), dtype=torch.uint8, device=v_bhsd.device)
     f8 = v_bhsd.to(torch.float8_e4m3fn)
     if torch.equal(f8.to(v_bhsd.dtype), v_bhsd):
         codes_t[..., :s] = f8.view(torch.uint8).transpose(-1, -2)
         if block_scale is not None:
-            return codes_t, block_scale, 1
-        return codes_t, v_scale_bhd.float().contiguous(), 0
+            return codes_t, block_scale, 1, True
+        return codes_t, v_scale_bhd.float().contiguous(), 0, True
     if block_scale is not None:
         raise ValueError("v_block_scale_bsh needs V in raw FP8 value units (E4M3 values in bf16)")
     codes, scale = fp8_per_channel_quant(v_bhsd.permute(0, 2, 1, 3).contiguous())  # (B,S,H,D), (B,H,D)
     codes_t[..., :s] = codes.view(torch.uint8).permute(0, 2, 3, 1)
-    return codes_t, (scale.float() * v_scale_bhd.float()).contiguous(), 0
+    return codes_t, (scale.float() * v_scale_bhd.float()).contiguous(), 0, False
 
 
 def fake_quant_attention_triton(
@@ -218,15 +228,26 @@ def triton_operands(q_bhsd, k_bhsd, v_bhsd_bf16, v_scale_bhd, *, sm_scale, p_max
                                   "correction (qm_bhgd / k_smooth_bhsd)")
 
     P = (S + 127) // 128 * 128
-    q_codes, q_scale, qblk, _ = _requant_qk(q_bhsd, block_m, P)
-    k_codes, k_scale, kblk, _ = _requant_qk(k_bhsd, block_m, P)
+    q_codes, q_scale, qblk, q_exact = _requant_qk(q_bhsd, block_m, P)
+    k_codes, k_scale, kblk, k_exact = _requant_qk(k_bhsd, block_m, P)
     if kblk != qblk:  # one block size for both (the kernel reads one fp8_block size)
         blk = min(qblk, kblk)
-        q_codes, q_scale, _, _ = _requant_qk(q_bhsd, blk, P)
-        k_codes, k_scale, _, _ = _requant_qk(k_bhsd, blk, P)
+        q_codes, q_scale, _, q_exact = _requant_qk(q_bhsd, blk, P)
+        k_codes, k_scale, _, k_exact = _requant_qk(k_bhsd, blk, P)
         qblk = blk
+    if not (q_exact and k_exact):
+        warnings.warn(f"Q/K are not fp8_block-dequantised values; re-quantised to {qblk}-row FP8 blocks "
+                      "(the reference runs bf16 dots on them)", RequantWarning, stacklevel=3)
     bscale = v_block_scale_bsh.permute(0, 2, 1).contiguous() if v_kind_block else None
-    v_codes_t, v_scale, v_kind = _v_codes(v_bhsd_bf16, v_scale_bhd, P, bscale)
+    v_codes_t, v_scale, v_kind, v_exact = _v_codes(v_bhsd_bf16, v_scale_bhd, P, bscale)
+    if not v_exact:
+        warnings.warn("V is not E4M3-valued; re-quantised to per-channel FP8 codes (the reference multiplies "
+                      "the bf16 values)", RequantWarning, stacklevel=3)
+    if has_v_alpha and v_kind == 0 and not bool((torch.isfinite(v_scale) & (v_scale > 0)).all()):
+        # the kernel holds the V-smoothing correction in the accumulator's
+        # units (alpha / v_scale) so the epilogue's per-channel multiply
+        # restores it; a zero or non-finite channel scale has no such form
+        raise ValueError("v_scale_bhd must be finite and > 0 in every channel when v_alpha is given")
     bias = rowmax = None
     if has_qm:
         ks_nhd = k_smooth_bhsd.permute(0, 2, 1, 3).contiguous()
@@ -262,4 +283,4 @@ def triton_operands(q_bhsd, k_bhsd, v_bhsd_bf16, v_scale_bhd, *, sm_scale, p_max
     return ops, cfg, init
 
 
-__all__ = ["fake_quant_attention_triton"]
+__all__ = ["fake_quant_attention_triton", "RequantWarning"]

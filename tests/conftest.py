@@ -26,9 +26,11 @@ def cpu_randn(*shape, seed=0, dtype=torch.bfloat16, scale=1.0):
 
 
 def cosine(a, b):
-    a = a.float().flatten()
-    b = b.float().flatten()
-    return torch.nn.functional.cosine_similarity(a.unsqueeze(0), b.unsqueeze(0)).item()
+    """Cosine similarity in float64 (a float32 reduction over ~10^6 elements is
+    off by ~10^-5)."""
+    a = a.double().flatten()
+    b = b.double().flatten()
+    return ((a @ b) / (a.norm() * b.norm()).clamp_min(1e-300)).item()
 
 
 def max_abs(a, b):

@@ -11,12 +11,18 @@ Tolerances (north star: cosine >= 0.9999, max |diff| <= 1e-2), see
   every |diff| <= 1e-2, or one bf16 ulp of the value where that is larger
   (both sides round an fp32 value to bf16); BLASST per-row skip counts and
   statistics exactly;
-* against the reference's own bf16-dequant scores: cosine >= 0.9999 for the
-  dense configurations, BLASST skip decisions equal outside rows within the
-  score perturbation of the threshold.  The element-wise gap to the reference
-  is recorded, not bounded: it is the reference's bf16 rounding of the
-  dequantised Q/K (attention.py:534-535) and the MFMA accumulation acting on
-  the scores, which an FP8-MFMA kernel cannot reproduce.
+* against the reference's own bf16-dequant scores, every configuration
+  (BLASST included): element-wise within the larger of the reference's own
+  bf16-vs-fp32 dequant gap and the MFMA score-error gap on the same rows plus
+  the strict tolerance, and the angle to the reference within the larger of
+  the two gaps' angles plus acos(0.9999) (``parity.reference_bound``); cosine
+  >= 0.9999 against the reference for the dense configurations wherever the
+  reference itself keeps 0.9999 against its exact-dequant variant; BLASST
+  skip decisions equal outside rows within the score perturbation of the
+  threshold.  The remaining element-wise gap is the reference's bf16
+  rounding of the dequantised Q/K (attention.py:534-535) and the MFMA
+  accumulation acting on the scores, which an FP8-MFMA kernel cannot
+  reproduce.
 Codes, scales and permutations are checked bit-exactly in the other GPU
 tests.
 """
@@ -38,17 +44,19 @@ MAXABS = parity.MAXABS
 
 
 def check_parity(out, q, k, v, cfg, label="", dev=None):
-    """Strict check against the replay; cosine against the reference (dense)."""
+    """Strict check against the replay; against the reference bounded by the
+    reference's own bf16-vs-fp32-dequant gap (every configuration); cosine
+    against the reference (dense)."""
     dev = dev or torch.device("cuda:0")
     ops, sm = parity.kernel_operands(q, k, v, cfg, dev)
     u = parity.kernel_scores(ops, cfg, sm)
-    c_rep, m_rep, _, _ = parity.check_against_replay(out, q, k, v, cfg, ops, u, label)
+    c_rep, m_rep, rep, dbg = parity.check_against_replay(out, q, k, v, cfg, ops, u, label)
     ref = opipe.fake_quant_attention(q, k, v, cfg)
-    fin = torch.isfinite(ref) & torch.isfinite(out)
-    c_ref = cosine(out[fin], ref[fin])
-    if cfg.blasst_lambda is None:
-        assert c_ref >= COS_MIN, f"{label}: vs reference cos={c_ref:.7f}"
-    return c_rep, m_rep, c_ref
+    ref32 = opipe.fake_quant_attention(q, k, v, cfg, qk_dequant_dtype=torch.float32)
+    st = parity.reference_bound(out, ref, ref32, rep, label, allowance=dbg["flip_allowance_nhd"])
+    if cfg.blasst_lambda is None and st["ref_self_cos"] >= COS_MIN:
+        assert st["cos_ref"] >= COS_MIN, f"{label}: vs reference cos={st['cos_ref']:.7f}"
+    return c_rep, m_rep, st["cos_ref"]
 
 
 def _cfg(**kw):
@@ -345,18 +353,22 @@ def test_reference_gap_comes_from_the_scores(gpu, name):
     assert max_abs(r32, ref) > MAXABS
 
 
+@pytest.mark.timeout(900)
 @pytest.mark.parametrize("config", [1, 2, 3, 4])
 def test_full_length_padded_wan_shapes(gpu, config):
     """BASELINE configs 1-4 at their real lengths (N = 32760, and 75600 for
     config 4, padded per the Wan hook: Q zero rows, K/V repeat the last row,
-    bench/wan_attention_hook.py:249-294), 2 heads, 256 rows of the padded
-    problem checked against the replay (strict), the reference (cosine, the
-    dense configurations) and, for BLASST, the per-row skip counts (exact)."""
+    bench/wan_attention_hook.py:249-294), 4 heads, 1024 random rows of the
+    padded problem plus, in every head, 64 caller rows spread over the last
+    256 real rows, checked against the replay (strict), the reference bounded
+    by its own bf16-vs-fp32-dequant gap on the same rows (every config,
+    BLASST included), the reference's cosine (the dense configurations) and,
+    for BLASST, the per-row skip counts (exact)."""
     from low_bit_fake_quant.attention_kernel import launch_attention
     from low_bit_fake_quant.wan import make_inputs, pad_qkv, workloads
     w = workloads()[config]
     cfg = w.cfg
-    q, k, v = make_inputs(w, seed=0, heads=2)
+    q, k, v = make_inputs(w, seed=0, heads=4)
     qp, kp, vp, n = pad_qkv(q, k, v, cfg)
     assert n == w.N and qp.shape[1] > n
     ops, sm = parity.kernel_operands(qp, kp, vp, cfg, gpu)
@@ -364,20 +376,29 @@ def test_full_length_padded_wan_shapes(gpu, config):
     res = launch_attention(ops, cfg, sm, torch.bfloat16, return_row_skips=bl)
     out, rsk = res if bl else (res, None)
     out = out.cpu()
-    rows = torch.randperm(ops.s, generator=torch.Generator().manual_seed(config))[:256]
-    caller, u, rep, ref, dbg_rep = parity.sampled_rows(qp, kp, vp, cfg, ops, rows, sm)
+    rows = torch.randperm(ops.s, generator=torch.Generator().manual_seed(config))[:1024]
+    caller, u, rep, ref, dbg_rep, ref32 = parity.sampled_rows(qp, kp, vp, cfg, ops, rows, sm, tail=64, n_real=n,
+                                                              with_ref32=True)
+    assert ((caller >= n - 256) & (caller < n)).sum(1).min() >= 64, "every head checks rows next to N"
     got = parity.gather_caller_rows(out, caller)
-    parity.strict_check(got, rep, f"config {config}",
-                        allowance=dbg_rep["flip_allowance"].permute(0, 2, 1, 3))
-    c_ref = cosine(got, ref)
-    print(f"config {config}: S={qp.shape[1]} rows=256 cos(kernel, ref)={c_ref:.7f} max|kernel - ref|="
-          f"{max_abs(got, ref):.3e}")
+    alw = dbg_rep["flip_allowance"].permute(0, 2, 1, 3)
+    parity.strict_check(got, rep, f"config {config}", allowance=alw)
+    # padding rows (Q zero rows past N) are sliced off by the caller
+    real = (caller < n).reshape(ops.b, ops.h, -1).permute(0, 2, 1)[..., None].expand_as(got)
+    keep = lambda t: torch.where(real, t.float(), torch.zeros((), dtype=torch.float32))  # noqa: E731
+    st = parity.reference_bound(keep(got), keep(ref), keep(ref32), keep(rep), f"config {config}", allowance=alw)
+    print(f"config {config}: S={qp.shape[1]} heads={ops.h} rows={caller.shape[1]} {st}")
     if bl:
         got_skips = torch.gather(rsk.cpu(), 1, caller)
         assert torch.equal(got_skips, dbg_rep["row_skips"].reshape(ops.b * ops.h, -1))
         print(f"config {config}: skip rate of the sample {got_skips.sum() / (got_skips.numel() * ops.s / 64):.3f}")
+    elif st["ref_self_cos"] >= COS_MIN:
+        assert st["cos_ref"] >= COS_MIN, f"config {config}: vs reference cos={st['cos_ref']:.7f}"
     else:
-        assert c_ref >= COS_MIN
+        # the reference itself misses 0.9999 against its exact-dequant variant on
+        # this sample: its own bf16 rounding of the dequantised Q/K is the gap, and
+        # the angle bound in reference_bound holds the kernel to it
+        print(f"config {config}: the reference's own bf16-vs-fp32 cosine {st['ref_self_cos']:.7f} < {COS_MIN}")
 
 
 @pytest.mark.parametrize("v_kind", [0, 2])

@@ -78,3 +78,32 @@ def test_mfma_32x32x64_layout_and_scales(gpu, scaled):
     assert err < 5e-4, f"relative error {err:.2e}"
     # the layout itself must be right: every element close to its own reference
     assert np.corrcoef(got.ravel(), ref.ravel())[0, 1] > 0.999999
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 48, 1 << 22])
+def test_hbm_stream_probe_moves_exactly_the_bytes(gpu, nbytes):
+    """lbfq_hbm_stream (the prepass ceiling probe): the copy mode copies the
+    bytes exactly, the write mode writes word i's index into its first dword
+    and nothing past the end, the read mode writes nothing; partial last
+    chunks included."""
+    from low_bit_fake_quant import _lib
+    lib = _lib.load()
+    st = _lib.stream_handle(gpu)
+    n16 = nbytes // 16
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (n16 + 4, 4), dtype=torch.int32, device=gpu)
+    sink = torch.zeros(256, dtype=torch.int32, device=gpu)
+    for mode in (0, 1, 2):
+        dst = torch.full((n16 + 4, 4), -7, dtype=torch.int32, device=gpu)
+        _lib.check(lib.lbfq_hbm_stream(mode, src.data_ptr(), dst.data_ptr(), nbytes, 64, sink.data_ptr(), st),
+                   "lbfq_hbm_stream")
+        torch.cuda.synchronize()
+        want = torch.full_like(dst, -7)
+        if mode == 1:
+            want[:n16] = 0
+            want[:n16, 0] = torch.arange(n16, dtype=torch.int32, device=gpu)
+        elif mode == 2:
+            want[:n16] = src[:n16]
+        assert torch.equal(dst, want), mode
+    with pytest.raises(ValueError, match="multiple of 16"):
+        _lib.check(lib.lbfq_hbm_stream(2, src.data_ptr(), dst.data_ptr(), 24, 64, sink.data_ptr(), st),
+                   "lbfq_hbm_stream")
