@@ -75,10 +75,6 @@ typedef struct {
   int mx_block;                            /* MX-QK columns per scale (8..D)    */
   int smoothed_stage;                      /* 0: after subtract, 1: after FWHT  */
   int scale_e8m0;                          /* MX modes: write E8M0 bytes, not fp32 */
-  int64_t h_begin, h_count;                /* heads [h_begin, h_begin + h_count) of */
-                                           /* the H (h_count 0: all), so a head     */
-                                           /* chunk can be processed by a pass pair */
-                                           /* while its input is still cached       */
 } lbfq_rowtile_params;
 
 int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream);

@@ -59,7 +59,6 @@ struct RowTileArgs {
   int scale_e8m0;
   uint32_t ntile;  // ceil(S / R)
   uint32_t nsub;   // S / sub_block (BLOCKVEC)
-  uint32_t h_begin, h_count;  // the heads this launch covers
 };
 
 __device__ __forceinline__ void store8(void* y, int dt, int64_t idx, const float v[8]) {
@@ -165,12 +164,13 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
   const int d0 = (lane % lpr) * 8;
   const int rl = lane / lpr;
 
-  // 32-bit index arithmetic: the grid (B * h_count * ntile workgroups,
-  // exactly) is below 2^31
+  // 32-bit index arithmetic: the grid (B * H * ntile workgroups, exactly) is
+  // below 2^31
   const uint32_t ntile = a.ntile;
+  const uint32_t H32 = static_cast<uint32_t>(a.H);
   uint32_t t = blockIdx.x;
-  const int64_t h = a.h_begin + t % a.h_count;
-  t /= a.h_count;
+  const int64_t h = t % H32;
+  t /= H32;
   const int64_t tile = t % ntile;
   const int64_t b = t / ntile;
   const int64_t bh = b * a.H + h;
@@ -663,13 +663,8 @@ extern "C" int lbfq_rowtile(const lbfq_rowtile_params* p, lbfq_stream_t stream) 
   a.mx_block = p->mx_block;
   a.smoothed_stage = p->smoothed_stage;
   a.scale_e8m0 = p->scale_e8m0;
-  const int64_t hc = p->h_count > 0 ? p->h_count : p->H;
-  LBFQ_CHECK_ARG(p->h_begin >= 0 && p->h_begin + hc <= p->H, "lbfq_rowtile: head range [%lld, %lld) outside H=%lld",
-                 (long long)p->h_begin, (long long)(p->h_begin + hc), (long long)p->H);
-  a.h_begin = static_cast<uint32_t>(p->h_begin);
-  a.h_count = static_cast<uint32_t>(hc);
   int64_t ntile = (p->S + p->R - 1) / p->R;
-  const int64_t ntiles = p->B * hc * ntile;
+  const int64_t ntiles = p->B * p->H * ntile;
   a.ntile = static_cast<uint32_t>(ntile);
   a.nsub = p->sub_mode == LBFQ_SUB_BLOCKVEC ? static_cast<uint32_t>(p->S / p->sub_block) : 0u;
   const int64_t nblocks = ntiles;  // one workgroup per tile

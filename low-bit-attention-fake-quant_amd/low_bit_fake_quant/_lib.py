@@ -49,7 +49,6 @@ class RowTileParams(ctypes.Structure):
         ("mx_block", _i32),
         ("smoothed_stage", _i32),
         ("scale_e8m0", _i32),
-        ("h_begin", _i64), ("h_count", _i64),
     ]
 
 

@@ -43,9 +43,7 @@ def rowtile(src: RowSource, *, R: int, smoothed: torch.Tensor | None = None, smo
             signs: torch.Tensor | None = None, hadamard: bool = False, had_scale: float = 1.0,
             quant_mode: int = _lib.Q_NONE, codes: torch.Tensor | None = None, codes_layout: int = _lib.LAYOUT_NHD,
             codes_spitch: int = 0, scale: torch.Tensor | None = None, scale_strides=(0, 0, 0, 0),
-            amax_table: torch.Tensor | None = None, mx_block: int = 32, scale_e8m0: bool = False,
-            heads: tuple[int, int] | None = None) -> None:
-    """``heads`` = (first, count): only those heads (all when None)."""
+            amax_table: torch.Tensor | None = None, mx_block: int = 32, scale_e8m0: bool = False) -> None:
     lib = _lib.load()
     x = src.x
     b, s, h, d = x.shape
@@ -65,7 +63,6 @@ def rowtile(src: RowSource, *, R: int, smoothed: torch.Tensor | None = None, smo
     p.mx_block = int(mx_block)
     p.smoothed_stage = int(smoothed_stage)
     p.scale_e8m0 = 1 if scale_e8m0 else 0
-    p.h_begin, p.h_count = (0, 0) if heads is None else (int(heads[0]), int(heads[1]))
     _lib.check(lib.lbfq_rowtile(p, _lib.stream_handle(x.device)), "lbfq_rowtile")
 
 
@@ -94,29 +91,20 @@ def column_mean(x: torch.Tensor, chunk: int = 256) -> torch.Tensor:
     return mean
 
 
-def channel_amax_table(b: int, h: int, d: int, device) -> torch.Tensor:
-    """A (B,H,D) channel-amax accumulator set to the amax floor (fp32 bits)."""
-    lib = _lib.load()
-    table = torch.empty((b, h, d), dtype=torch.int32, device=device)
-    _lib.check(lib.lbfq_fill_u32(table.data_ptr(), table.numel(), AMAX_FLOOR_BITS, _lib.stream_handle(device)),
-               "lbfq_fill_u32")
-    return table
-
-
-def channel_amax(src: RowSource, tile: int = 1024, table: torch.Tensor | None = None,
-                 heads: tuple[int, int] | None = None) -> torch.Tensor:
+def channel_amax(src: RowSource, tile: int = 1024) -> torch.Tensor:
     """Per-(b,h,d) max |x| over S (floored at fp32(1e-4)) as uint32 fp32 bits.
 
     One workgroup per `tile` rows of a head (the row-tile kernel's largest
     tile: fewest workgroups and atomics; 64.5 against 72 us at tile 256 for
     40 x 32768 x 128 bf16 on an MI355X).  The max does not depend on the
-    tiling, so every tile size gives the same bits.  ``table`` (already
-    filled with the floor) and ``heads`` restrict the pass to a head range.
+    tiling, so every tile size gives the same bits.
     """
+    lib = _lib.load()
     b, s, h, d = src.x.shape
-    if table is None:
-        table = channel_amax_table(b, h, d, src.x.device)
-    rowtile(src, R=tile, quant_mode=_lib.Q_CHANNEL_AMAX, amax_table=table, heads=heads)
+    table = torch.empty((b, h, d), dtype=torch.int32, device=src.x.device)
+    _lib.check(lib.lbfq_fill_u32(table.data_ptr(), table.numel(), AMAX_FLOOR_BITS,
+                                 _lib.stream_handle(src.x.device)), "lbfq_fill_u32")
+    rowtile(src, R=tile, quant_mode=_lib.Q_CHANNEL_AMAX, amax_table=table)
     return table
 
 

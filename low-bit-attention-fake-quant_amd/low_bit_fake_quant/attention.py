@@ -31,8 +31,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from ._ops import (RowSource, channel_amax, channel_amax_table, colsum_mean, column_mean, hadamard_scale, qmk,
-                   round_up, rowtile)
+from ._ops import RowSource, channel_amax, colsum_mean, column_mean, hadamard_scale, qmk, round_up, rowtile
 from .attention_kernel import launch_attention, parse_blasst_fill, v_tile_colsum, validate_kernel_config
 from .config import QuantConfig
 from .hadamard import apply_qk_hadamard, qk_signs_device
@@ -219,11 +218,6 @@ def _quant_qk_codes(src: RowSource, cfg: QuantConfig, P: int, *, signs):
     return codes, scale
 
 
-# input bytes of one head chunk of the V channel quantiser (two passes per
-# chunk; the chunk stays in the MALL between them)
-V_CHUNK_BYTES = 64 << 20
-
-
 def _quant_v_codes(src: RowSource, cfg: QuantConfig, P: int):
     """Quantise V into transposed codes (B,H,D,P) and the kernel's scales:
     channel (B,H,D) fp32, fp8_block (B,H,S/vb) fp32, mxfp8 (B,H,S/vb,D) E8M0.
@@ -232,21 +226,10 @@ def _quant_v_codes(src: RowSource, cfg: QuantConfig, P: int):
     dev = src.x.device
     codes = (torch.zeros if P > s else torch.empty)((b, h, d, P), dtype=torch.uint8, device=dev)
     if cfg.v_quant == "fp8_channel":
-        # Two passes per head chunk: the channel amax over all S, then the codes.
-        # A chunk of about V_CHUNK_BYTES of input is still in the 256 MB MALL
-        # when its second pass reads it, so V comes from HBM once.
-        table = channel_amax_table(b, h, d, dev)
+        table = channel_amax(src)
         scale = torch.empty((b, h, d), dtype=torch.float32, device=dev)
-        per_head = b * s * d * src.x.element_size()
-        hc = max(1, min(h, V_CHUNK_BYTES // per_head))
-        for h0 in range(0, h, hc):
-            n = min(hc, h - h0)
-            # enough amax workgroups to fill the chip for small chunks (any tile size gives the same bits)
-            r_amax = 1024 if n * ((s + 1023) // 1024) >= 512 else 256
-            channel_amax(src, tile=r_amax, table=table, heads=(h0, n))
-            rowtile(src, R=64, quant_mode=_lib.Q_CHANNEL, codes=codes, codes_layout=_lib.LAYOUT_BHDS,
-                    codes_spitch=P, scale=scale, scale_strides=(scale.stride(0), 0, scale.stride(1), scale.stride(2)),
-                    amax_table=table, heads=(h0, n))
+        rowtile(src, R=64, quant_mode=_lib.Q_CHANNEL, codes=codes, codes_layout=_lib.LAYOUT_BHDS, codes_spitch=P,
+                scale=scale, scale_strides=(scale.stride(0), 0, scale.stride(1), scale.stride(2)), amax_table=table)
         return codes, scale, 0, 0
     if cfg.v_quant == "fp8_block":
         vb = cfg.v_fp8_block_size
