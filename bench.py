@@ -321,6 +321,42 @@ def hbm_ceiling(dev, nbytes: int = 1 << 31, grids=(1024, 2048, 4096, 8192)):
     return res
 
 
+ISSUE_OPS = ("v_mul_f32", "v_add_f32", "v_fma_f32", "v_max3_f32", "v_exp_f32", "v_cvt_pk_fp8_f32",
+             "v_permlane32_swap", "mfma_f32_32x32x64_f8", "tile_mix", "tile_mix_valu_only")
+
+
+def issue_costs(dev, iters: int = 2000):
+    """lbfq_issue_probe on one CU: cycles per wave-instruction at the SIMD for
+    each instruction class the attention step is made of, and cycles per
+    wave-tile of the step's inherent mix (8 MFMAs + 198 VALU, all independent:
+    a perfect schedule), at 1 and 2 waves per SIMD (the attention kernel runs
+    2).  Per SIMD: (latest end - earliest start of its waves) / (waves x
+    iterations x instructions per iteration)."""
+    from low_bit_fake_quant import _lib
+    lib = _lib.load()
+    st = _lib.stream_handle(dev)
+    sink = torch.zeros(512, dtype=torch.float32, device=dev)
+    rec = torch.zeros(8 * 3, dtype=torch.int64, device=dev)
+    per_iter = [16] * 7 + [8, 1, 1]
+    out = {}
+    for w in (1, 2):
+        row = {}
+        for op, name in enumerate(ISSUE_OPS):
+            _lib.check(lib.lbfq_issue_probe(op, w, iters, rec.data_ptr(), sink.data_ptr(), st), "lbfq_issue_probe")
+            torch.cuda.synchronize()
+            r = rec[:3 * 4 * w].view(4 * w, 3).cpu().tolist()
+            worst = 0.0
+            for simd in range(4):
+                ws = [x for x in r if x[2] == simd]
+                if len(ws) == w:
+                    span = max(x[1] for x in ws) - min(x[0] for x in ws)
+                    worst = max(worst, span / (w * iters * per_iter[op]))
+            row[name] = worst
+        out[f"{w}_wave_per_simd"] = row
+        log(f"issue costs at {w} wave(s)/SIMD: " + ", ".join(f"{k} {v:.2f}" for k, v in row.items()))
+    return out
+
+
 def traffic_from_profile(config: int):
     """HBM bytes per attention launch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, calibrated by a copy of known size), or None."""
@@ -334,7 +370,7 @@ def traffic_from_profile(config: int):
     return None
 
 
-def clock_sample(ops, cfg, sm_scale, launches, flops, launch_attention) -> int:
+def clock_sample(ops, cfg, sm_scale, launches, flops, launch_attention, quiet=False):
     """Shader clock under a long run of the attention kernel: rocm-smi is
     sampled from a thread while `launches` launches run back to back.  The
     datasheet FP8 peak (5.0 PFLOP/s) is quoted at 2.4 GHz; the rate is also
@@ -382,11 +418,14 @@ def clock_sample(ops, cfg, sm_scale, launches, flops, launch_attention) -> int:
     peak_at_clk = FP8_PEAK_TFLOPS * med / 2400.0
     for t, c, mc in samples:
         log(f"t={t:5.2f}s sclk {c} MHz mclk {mc} MHz")
-    print(json.dumps({"launches": launches, "ms_per_launch": ms, "TFLOPs": tflops,
-                      "sclk_idle_MHz": idle[0] if idle else None, "sclk_median_MHz": med,
-                      "sclk_samples": len(samples), "frac_of_fp8_peak_2400MHz": tflops / FP8_PEAK_TFLOPS,
-                      "fp8_peak_at_median_clock_TFLOPs": peak_at_clk,
-                      "frac_of_clock_scaled_peak": tflops / peak_at_clk}))
+    res = {"launches": launches, "ms_per_launch": ms, "TFLOPs": tflops,
+           "sclk_idle_MHz": idle[0] if idle else None, "sclk_median_MHz": med,
+           "sclk_samples": len(samples), "frac_of_fp8_peak_2400MHz": tflops / FP8_PEAK_TFLOPS,
+           "fp8_peak_at_median_clock_TFLOPs": peak_at_clk,
+           "frac_of_clock_scaled_peak": tflops / peak_at_clk}
+    if quiet:
+        return res
+    print(json.dumps(res))
     return 0
 
 
@@ -403,6 +442,10 @@ def main() -> int:
                     help="skip timing configs 1, 3 and 4 beside the headline config")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="driver for rocprofv3 --pmc passes: a 1 GiB calibration copy, then one attention launch")
+    ap.add_argument("--issue-floor", action="store_true",
+                    help="issue costs of the attention step's instruction classes and of its inherent per-tile mix "
+                         "(lbfq_issue_probe), the config's attention timed under a clock sample, and the floor they "
+                         "imply; one JSON line")
     ap.add_argument("--hbm-ceiling", action="store_true",
                     help="only the HBM streaming probe (read / write / copy), one JSON line")
     ap.add_argument("--trace-timed-only", action="store_true",
@@ -463,6 +506,28 @@ def main() -> int:
 
     if args.clock_sample:
         return clock_sample(ops, cfg, sm_scale, args.clock_sample, attention_flops(n_real, h, d, b), launch_attention)
+
+    if args.issue_floor:
+        costs = issue_costs(dev)
+        props = torch.cuda.get_device_properties(dev)
+        simds = props.multi_processor_count * 4
+        # (wave of 32 queries, 64-key tile) pairs per SIMD: workgroups of 4 waves x 128 queries
+        wave_tiles = b * h * ((s + 127) // 128) * 4 * ((s + 63) // 64) / simds
+        info = clock_sample(ops, cfg, sm_scale, 120, attention_flops(n_real, h, d, b), launch_attention,
+                            quiet=True)
+        mhz = info["sclk_median_MHz"]
+        tile = costs["2_wave_per_simd"]["tile_mix"]
+        floor_ms = tile * wave_tiles / (mhz * 1e3)
+        kernel_cycles = info["ms_per_launch"] * 1e-3 * mhz * 1e6 / wave_tiles
+        print(json.dumps({"issue_costs_cycles": costs, "simds": simds, "wave_tiles_per_simd": wave_tiles,
+                          "sclk_median_MHz": mhz, "attention_ms": info["ms_per_launch"],
+                          "attention_cycles_per_wave_tile": kernel_cycles,
+                          "floor_cycles_per_wave_tile": tile, "floor_ms_at_sampled_clock": floor_ms,
+                          "floor_ms_at_2400MHz": tile * wave_tiles / 2.4e6,
+                          "floor_frac_of_fp8_peak_at_sampled_clock":
+                              attention_flops(n_real, h, d, b) / (floor_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS,
+                          "kernel_over_floor": kernel_cycles / tile}))
+        return 0
 
     # ---- attention kernel: the timed step ----------------------------------
     out = launch_attention(ops, cfg, sm_scale, torch.bfloat16)

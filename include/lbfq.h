@@ -323,6 +323,16 @@ int lbfq_blasst_attend(const lbfq_blasst_attend_params* p, lbfq_stream_t stream)
  * pointers. */
 int lbfq_hbm_stream(int mode, const void* src, void* dst, int64_t bytes, int grid, uint32_t* sink,
                     lbfq_stream_t stream);
+/* Issue-cost probe (no counterpart in the reference: it measures the floor
+ * the attention kernel is held against).  One workgroup of 4 * waves_per_simd
+ * waves (1 or 2 per SIMD of one CU) runs `iters` iterations of independent
+ * instructions of class `op` -- 0 v_mul_f32, 1 v_add_f32, 2 v_fma_f32,
+ * 3 v_max3_f32, 4 v_exp_f32, 5 v_cvt_pk_fp8_f32, 6 v_permlane32_swap (16 per
+ * iteration), 7 FP8 MFMA 32x32x64 (8 per iteration), 8 the attention step's
+ * inherent per-tile mix (8 MFMAs + 198 VALU), 9 that mix's VALU part.
+ * rec: 3 int64 per wave (s_memtime at start, at end, SIMD id); sink: one
+ * float per thread. */
+int lbfq_issue_probe(int op, int waves_per_simd, int iters, long long* rec, float* sink, lbfq_stream_t stream);
 
 /* ---- building-block self tests (GPU unit tests of compiler builtins) ------ */
 /* E4M3 conversion of n fp32 values (n even) by the hardware converter. */

@@ -9,6 +9,10 @@
 // * hbm_stream: read-only / write-only / copy streams of 16-byte words, the
 //   measured HBM ceiling the prepass is held against (no reference
 //   counterpart).
+// * issue_probe: cycles per wave-instruction of the instruction classes the
+//   attention step is made of, and of the step's inherent per-tile mix, at a
+//   given number of waves per SIMD (no reference counterpart: it measures the
+//   floor the attention kernel is held against).
 #include "lbfq_common.h"
 #include "../../include/lbfq.h"
 
@@ -274,7 +278,132 @@ __global__ void __launch_bounds__(kStreamThreads) hbm_stream_kernel(const uint4*
   }
 }
 
+// Issue-cost probe.  One workgroup of 4 * W waves runs on one CU, so each of
+// its four SIMDs holds W waves; every wave runs `iters` iterations of a loop
+// body of independent instructions (16 chains of one class, or the tile mix
+// below) between two s_memtime reads and records (start, end, SIMD id).  The
+// host takes, per SIMD, (latest end - earliest start) / (waves x iterations x
+// instructions per iteration): the SIMD's cost per wave-instruction.  The
+// VALU chains never touch the MFMA accumulators, so no operand of an
+// in-flight MFMA is read.
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+#define LBFQ_P_MUL(i) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x[(i) & 31]) : "v"(c));
+#define LBFQ_P_ADD(i) asm volatile("v_add_f32 %0, %0, %1" : "+v"(x[(i) & 31]) : "v"(c));
+#define LBFQ_P_FMA(i) asm volatile("v_fma_f32 %0, %0, %1, %1" : "+v"(x[(i) & 31]) : "v"(c));
+#define LBFQ_P_MAX3(i) asm volatile("v_max3_f32 %0, %0, %1, %0" : "+v"(x[(i) & 31]) : "v"(c));
+#define LBFQ_P_MAX(i) asm volatile("v_max_f32 %0, %0, %1" : "+v"(x[(i) & 31]) : "v"(c));
+#define LBFQ_P_EXP(i) asm volatile("v_exp_f32 %0, %0" : "+v"(x[(i) & 31]));
+#define LBFQ_P_CVT(i) asm volatile("v_cvt_pk_fp8_f32 %0, %0, %1" : "+v"(x[(i) & 31]) : "v"(c));
+#define LBFQ_P_PERM(i) asm volatile("v_permlane32_swap_b32 %0, %1" : "+v"(x[(i) & 31]), "+v"(x[((i) + 1) & 31]));
+
+// OP: 0 mul, 1 add, 2 fma, 3 max3, 4 exp, 5 cvt_pk_fp8, 6 permlane32_swap (16
+// per iteration); 7 FP8 MFMA 32x32x64 (8 per iteration, four accumulator
+// chains); 8 the attention step's inherent per-tile mix: 8 MFMAs, 32 fma,
+// 16 max3 + 3 max, 34 exp, 16 cvt, 32 add, 64 mul, 1 permlane (the work of
+// one wave on a 32-query x 64-key tile, dynamic P); 9 its VALU part alone.
+template <int OP>
+__global__ void __launch_bounds__(512) issue_probe_kernel(float* sink, int iters, long long* rec) {
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) x[i] = threadIdx.x * 0.001f + i;
+  const float c = 1.0000001f;
+  v8i_t a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { a[i] = 0x38383838 + static_cast<int>(threadIdx.x); b[i] = 0x38383838; }
+  v16f_t acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+  unsigned hw;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+  __syncthreads();
+  const long long t0 = clock64();
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (OP <= 6) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if constexpr (OP == 0) LBFQ_P_MUL(i)
+        if constexpr (OP == 1) LBFQ_P_ADD(i)
+        if constexpr (OP == 2) LBFQ_P_FMA(i)
+        if constexpr (OP == 3) LBFQ_P_MAX3(i)
+        if constexpr (OP == 4) LBFQ_P_EXP(i)
+        if constexpr (OP == 5) LBFQ_P_CVT(i)
+        if constexpr (OP == 6) LBFQ_P_PERM(2 * i)
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        if constexpr (OP == 7 || OP == 8)
+          acc[g & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[g & 3], 0, 0, 0, 127, 0, 127);
+        if constexpr (OP == 8 || OP == 9) {
+          const int o = 4 * g;
+          LBFQ_P_FMA(o) LBFQ_P_FMA(o + 1) LBFQ_P_FMA(o + 2) LBFQ_P_FMA(o + 3)
+          LBFQ_P_MAX3(o) LBFQ_P_MAX3(o + 1)
+          LBFQ_P_EXP(o) LBFQ_P_EXP(o + 1) LBFQ_P_EXP(o + 2) LBFQ_P_EXP(o + 3)
+          LBFQ_P_CVT(o) LBFQ_P_CVT(o + 1)
+          LBFQ_P_ADD(o) LBFQ_P_ADD(o + 1) LBFQ_P_ADD(o + 2) LBFQ_P_ADD(o + 3)
+          LBFQ_P_MUL(o) LBFQ_P_MUL(o + 1) LBFQ_P_MUL(o + 2) LBFQ_P_MUL(o + 3)
+          LBFQ_P_MUL(o + 4) LBFQ_P_MUL(o + 5) LBFQ_P_MUL(o + 6) LBFQ_P_MUL(o + 7)
+        }
+      }
+      if constexpr (OP == 8 || OP == 9) {
+        LBFQ_P_EXP(1) LBFQ_P_EXP(2) LBFQ_P_MAX(3) LBFQ_P_MAX(4) LBFQ_P_MAX(5) LBFQ_P_PERM(6)
+      }
+    }
+  }
+  const long long t1 = clock64();
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) s += x[i];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += acc[j][r];
+  sink[threadIdx.x] = s;
+  if ((threadIdx.x & 63) == 0) {
+    const int w = threadIdx.x >> 6;
+    rec[3 * w] = t0;
+    rec[3 * w + 1] = t1;
+    rec[3 * w + 2] = (hw >> 4) & 3;  // HW_ID.SIMD_ID
+  }
+}
+
+#undef LBFQ_P_MUL
+#undef LBFQ_P_ADD
+#undef LBFQ_P_FMA
+#undef LBFQ_P_MAX3
+#undef LBFQ_P_MAX
+#undef LBFQ_P_EXP
+#undef LBFQ_P_CVT
+#undef LBFQ_P_PERM
+
 }  // namespace
+
+extern "C" int lbfq_issue_probe(int op, int waves_per_simd, int iters, long long* rec, float* sink,
+                                lbfq_stream_t stream) {
+  LBFQ_CHECK_ARG(op >= 0 && op <= 9, "lbfq_issue_probe: op must be in [0, 9]");
+  LBFQ_CHECK_ARG(waves_per_simd == 1 || waves_per_simd == 2, "lbfq_issue_probe: 1 or 2 waves per SIMD");
+  LBFQ_CHECK_ARG(iters > 0 && rec && sink, "lbfq_issue_probe: bad args");
+  const dim3 g(1), blk(static_cast<unsigned>(256 * waves_per_simd));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (op) {
+    case 0: hipLaunchKernelGGL(issue_probe_kernel<0>, g, blk, 0, st, sink, iters, rec); break;
+    case 1: hipLaunchKernelGGL(issue_probe_kernel<1>, g, blk, 0, st, sink, iters, rec); break;
+    case 2: hipLaunchKernelGGL(issue_probe_kernel<2>, g, blk, 0, st, sink, iters, rec); break;
+    case 3: hipLaunchKernelGGL(issue_probe_kernel<3>, g, blk, 0, st, sink, iters, rec); break;
+    case 4: hipLaunchKernelGGL(issue_probe_kernel<4>, g, blk, 0, st, sink, iters, rec); break;
+    case 5: hipLaunchKernelGGL(issue_probe_kernel<5>, g, blk, 0, st, sink, iters, rec); break;
+    case 6: hipLaunchKernelGGL(issue_probe_kernel<6>, g, blk, 0, st, sink, iters, rec); break;
+    case 7: hipLaunchKernelGGL(issue_probe_kernel<7>, g, blk, 0, st, sink, iters, rec); break;
+    case 8: hipLaunchKernelGGL(issue_probe_kernel<8>, g, blk, 0, st, sink, iters, rec); break;
+    default: hipLaunchKernelGGL(issue_probe_kernel<9>, g, blk, 0, st, sink, iters, rec); break;
+  }
+  LBFQ_LAUNCH_CHECK("lbfq_issue_probe");
+  return 0;
+}
 
 extern "C" int lbfq_hbm_stream(int mode, const void* src, void* dst, int64_t bytes, int grid, uint32_t* sink,
                                lbfq_stream_t stream) {

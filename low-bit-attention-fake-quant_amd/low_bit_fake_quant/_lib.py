@@ -148,6 +148,7 @@ _SIGS = {
     "lbfq_blasst_keep": (_i32, [_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp]),
     "lbfq_blasst_attend": (_i32, [ctypes.POINTER(BlasstAttendParams), _vp]),
     "lbfq_hbm_stream": (_i32, [_i32, _vp, _vp, _i64, _i32, _vp, _vp]),
+    "lbfq_issue_probe": (_i32, [_i32, _i32, _i32, _vp, _vp, _vp]),
     "lbfq_selftest_cvt_fp8": (_i32, [_vp, _i64, _vp, _vp]),
     "lbfq_selftest_mfma": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp]),
 }

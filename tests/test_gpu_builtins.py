@@ -107,3 +107,28 @@ def test_hbm_stream_probe_moves_exactly_the_bytes(gpu, nbytes):
     with pytest.raises(ValueError, match="multiple of 16"):
         _lib.check(lib.lbfq_hbm_stream(2, src.data_ptr(), dst.data_ptr(), 24, 64, sink.data_ptr(), st),
                    "lbfq_hbm_stream")
+
+
+@pytest.mark.parametrize("op", [0, 4, 7, 8])
+def test_issue_probe_records_every_wave(gpu, op):
+    """lbfq_issue_probe (the attention floor measurement): at 2 waves per
+    SIMD every wave records a positive s_memtime span and a SIMD id, each of
+    the 4 SIMDs holds 2 waves, and the per-instruction cost is plausible
+    (at least 1 cycle, an MFMA at least the 32x32x64 FP8 rate of 64 cycles
+    less 10%)."""
+    from low_bit_fake_quant import _lib
+    lib = _lib.load()
+    rec = torch.zeros(8 * 3, dtype=torch.int64, device=gpu)
+    sink = torch.zeros(512, dtype=torch.float32, device=gpu)
+    iters = 200
+    _lib.check(lib.lbfq_issue_probe(op, 2, iters, rec.data_ptr(), sink.data_ptr(), _lib.stream_handle(gpu)),
+               "lbfq_issue_probe")
+    torch.cuda.synchronize()
+    r = rec.view(8, 3).cpu()
+    assert (r[:, 1] > r[:, 0]).all()
+    assert sorted(r[:, 2].tolist()) == [0, 0, 1, 1, 2, 2, 3, 3]
+    per_iter = {0: 16, 4: 16, 7: 8, 8: 1}[op]
+    cost = (r[:, 1].max() - r[:, 0].min()).item() / (8 * iters * per_iter) * 4
+    assert cost >= (57.6 if op == 7 else 1.0)
+    with pytest.raises(ValueError, match="1 or 2 waves"):
+        _lib.check(lib.lbfq_issue_probe(0, 3, 1, rec.data_ptr(), sink.data_ptr(), _lib.stream_handle(gpu)), "x")
