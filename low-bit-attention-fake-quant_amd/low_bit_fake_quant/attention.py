@@ -394,8 +394,9 @@ def _dequant_v(fp8, scale, meta, dtype):
 def _attention_fp32(qb, kb, vb, sm_scale, *, corr_q=None, corr_k=None, group=None, chunk=512, p_dtype=None):
     """softmax(q k^T * scale [+ corr]) v over BHSD tensors in fp32 with contiguous
     operands, chunked over queries (bounded memory).  ``p_dtype`` rounds the
-    probabilities before the PV product (the reference's chunked path casts P to
-    the SDPA dtype, attention.py:318-319)."""
+    main scores (before the scale and the correction) and the probabilities
+    before the PV product to the SDPA dtype, as the reference's chunked path
+    does (attention.py:314, 318)."""
     B, H, S, D = qb.shape
     kT = kb.float().transpose(-2, -1).contiguous()
     vf = vb.float().contiguous()
@@ -404,7 +405,12 @@ def _attention_fp32(qb, kb, vb, sm_scale, *, corr_q=None, corr_k=None, group=Non
     grp_idx = torch.arange(S, device=qb.device) // group if group else None
     for m0 in range(0, S, chunk):
         m1 = min(m0 + chunk, S)
-        scores = torch.matmul(qb[:, :, m0:m1].float().contiguous(), kT) * sm_scale
+        scores = torch.matmul(qb[:, :, m0:m1].float().contiguous(), kT)
+        if p_dtype is not None:
+            # the reference's main term is a matmul of the sdpa-dtype operands,
+            # whose output is in that dtype (attention.py:314)
+            scores = scores.to(p_dtype).float()
+        scores = scores * sm_scale
         if corr_q is not None:
             scores = scores + torch.matmul(corr_q[:, :, grp_idx[m0:m1]].float().contiguous(), ksT) * sm_scale
         p = torch.softmax(scores, dim=-1)

@@ -203,7 +203,10 @@ def sdpa_path(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype):
     ksb = k_work.permute(*perm).float()
     vb = v_deq.permute(*perm).float()
     grp = torch.arange(s) // block_q
-    s_main = torch.matmul(qb, kb.transpose(-2, -1)) * sm_scale
+    # attention.py:314: a matmul of the sdpa-dtype operands, its output rounded
+    # to that dtype, then scaled in fp32
+    s_main = torch.matmul(q_deq.permute(*perm).contiguous(),
+                          k_deq.permute(*perm).transpose(-2, -1).contiguous()).float() * sm_scale
     s_corr = torch.matmul(qmb[:, :, grp], ksb.transpose(-2, -1)) * sm_scale
     p = torch.softmax(s_main + s_corr, dim=-1).to(sdpa_dtype).float()
     return torch.matmul(p, vb).to(sdpa_dtype).permute(*perm).contiguous()
