@@ -231,6 +231,59 @@ int lbfq_v_tile_colsum(const uint8_t* v_codes_t, int64_t BH, int64_t S, int64_t 
 int lbfq_attention_scores(const lbfq_attn_params* p, const int32_t* rows, int64_t n_rows, float* u,
                           lbfq_stream_t stream);
 
+/* ---- path A: dequantised SDPA, P not quantised -------------------------------
+ * Replaces the dequantisation of _fake_quant_attention_sdpa (attention.py:
+ * 276-286: _dequant_qk / _dequant_v into the SDPA dtype, quant_triton.py:
+ * 81-109, 180-198, 275-298, 373-396, then the V block means added in that
+ * dtype).  Codes and scales in the layouts of lbfq_attn_params (the prepass
+ * writes them); outputs in the SDPA dtype: q_out, k_out (B,H,s_pitch,D) and
+ * v_t_out (B,H,D,s_pitch), rows / keys [S, s_pitch) zero. */
+typedef struct {
+  int64_t B, H, S, D;             /* D in {64, 128}                                */
+  int64_t s_pitch;                /* multiple of 128, >= S                         */
+  const uint8_t* q_codes;         /* (B,H,s_pitch,D)                               */
+  const uint8_t* k_codes;         /* (B,H,s_pitch,D)                               */
+  const uint8_t* v_codes_t;       /* (B,H,D,s_pitch)                               */
+  int qk_mx;                      /* 0: fp8_block, 1: MX E8M0 along D              */
+  const void* q_scale;            /* fp8_block (B,H,S/qk_block) fp32;              */
+  const void* k_scale;            /* mx (B,H,s_pitch,D/qk_block) E8M0 bytes        */
+  int qk_block;                   /* fp8_block rows (dividing S) / MX columns      */
+  int v_kind;                     /* 0 channel, 1 fp8_block, 2 mx                  */
+  const void* v_scale;            /* channel (B,H,D) fp32; block (B,H,S/vb) fp32;  */
+                                  /* mx (B,H,S/vb,D) E8M0 bytes                    */
+  int v_block;                    /* rows per V scale, dividing S                  */
+  const float* v_alpha;           /* (B,H,S/v_smooth_block,D) fp32 V block means,  */
+                                  /* or NULL                                       */
+  int v_smooth_block;
+  int sdpa_dtype;                 /* 1 fp16, 2 bf16                                */
+  void* q_out; void* k_out; void* v_t_out;
+} lbfq_sdpa_dequant_params;
+
+int lbfq_sdpa_dequant(const lbfq_sdpa_dequant_params* p, lbfq_stream_t stream);
+
+/* Replaces the attention of _fake_quant_attention_sdpa (attention.py:288-319):
+ * without qk_bias, F.scaled_dot_product_attention over the dequantised
+ * tensors with P in fp32 (:289-294); with qk_bias, the chunked Q-smoothing
+ * branch (:296-319): scores = dtype(q.k) * sm_scale + qm.K_s * sm_scale,
+ * P = dtype(softmax), O = P V.  Output NHD (B,S,H,D), rounded to the SDPA
+ * dtype and stored in out_dtype. */
+typedef struct {
+  int64_t B, H, S, D, s_pitch;
+  const void* q;                  /* (B,H,s_pitch,D) sdpa dtype, rows >= S zero    */
+  const void* k;                  /* (B,H,s_pitch,D)                               */
+  const void* v_t;                /* (B,H,D,s_pitch), keys >= S zero               */
+  int sdpa_dtype;                 /* 1 fp16, 2 bf16                                */
+  float sm_scale;
+  const float* qk_bias;           /* (B,H,groups,s_pitch) qm.K_s*sm_scale*log2(e)  */
+                                  /* (lbfq_qmk), or NULL                           */
+  int64_t groups;                 /* qm groups                                     */
+  int q_group;                    /* rows per qm group (> 0)                       */
+  void* out; int out_dtype;       /* NHD (B,S,H,D)                                 */
+  const int32_t* out_row_map;     /* (B*H, S): output row of reordered query, or NULL */
+} lbfq_sdpa_params;
+
+int lbfq_sdpa_fwd(const lbfq_sdpa_params* p, lbfq_stream_t stream);
+
 /* ---- diagnostics -------------------------------------------------------------
  * Replaces p_requant.py:44-73 (p_requant_rows, kernel :12-41).  scores is
  * (B, M, N) of dtype `dtype` with element strides ss*; p (E4M3 bytes) has

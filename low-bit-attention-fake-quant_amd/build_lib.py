@@ -46,6 +46,7 @@ UNITS = {
     "lbfq_attn_b128_p0.hip": ATTN_FLAGS,
     "lbfq_attn_b128_p1.hip": ATTN_FLAGS,
     "lbfq_attn_b128_p2.hip": ATTN_FLAGS,
+    "lbfq_sdpa.hip": ["-ffp-contract=off"],
 }
 
 

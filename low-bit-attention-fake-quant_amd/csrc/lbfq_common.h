@@ -54,6 +54,16 @@ __device__ __forceinline__ float round_to_dtype(float v, int dt) {
   return v;
 }
 
+// v as a materialised fp32 register value.  Before a narrowing to fp16 the
+// compiler otherwise selects fptrunc(a * b) (and a +- b) as a mixed-precision
+// FMA with a +0 addend: that rounds the exact result once instead of the
+// fp32 result (a double-rounding difference at fp16 ties) and turns a -0
+// product into +0.
+__device__ __forceinline__ float as_f32(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 __device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dt, float v) {
   if (dt == kBF16) reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
   else if (dt == kF16) reinterpret_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v);

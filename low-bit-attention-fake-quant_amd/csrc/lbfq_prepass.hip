@@ -241,7 +241,7 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
         mm[4] = m1.x; mm[5] = m1.y; mm[6] = m1.z; mm[7] = m1.w;
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) x[k] = round_dt<DT>(x[k] - mm[k]);
+      for (int k = 0; k < 8; ++k) x[k] = round_dt<DT>(as_f32(x[k] - mm[k]));
     }
     if (!tile_full) {
 #pragma unroll
@@ -275,7 +275,7 @@ __global__ void __launch_bounds__(kTileWaves * 64) rowtile_kernel(RowTileArgs a)
         }
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) x[k] = round_dt<DT>(x[k] * a.had_scale);
+      for (int k = 0; k < 8; ++k) x[k] = round_dt<DT>(as_f32(x[k] * a.had_scale));
       if (store_smoothed && sm1 && okp) store8(a.smoothed, DT, ((b * a.S + s_out) * a.H + h) * a.D + d0, x);
     }
   };

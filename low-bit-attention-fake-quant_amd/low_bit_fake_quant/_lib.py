@@ -120,6 +120,32 @@ class BlasstAttendParams(ctypes.Structure):
     ]
 
 
+class SdpaDequantParams(ctypes.Structure):
+    _fields_ = [
+        ("B", _i64), ("H", _i64), ("S", _i64), ("D", _i64), ("s_pitch", _i64),
+        ("q_codes", _vp), ("k_codes", _vp), ("v_codes_t", _vp),
+        ("qk_mx", _i32), ("q_scale", _vp), ("k_scale", _vp), ("qk_block", _i32),
+        ("v_kind", _i32), ("v_scale", _vp), ("v_block", _i32),
+        ("v_alpha", _vp), ("v_smooth_block", _i32),
+        ("sdpa_dtype", _i32),
+        ("q_out", _vp), ("k_out", _vp), ("v_t_out", _vp),
+    ]
+
+
+class SdpaParams(ctypes.Structure):
+    _fields_ = [
+        ("B", _i64), ("H", _i64), ("S", _i64), ("D", _i64), ("s_pitch", _i64),
+        ("q", _vp), ("k", _vp), ("v_t", _vp),
+        ("sdpa_dtype", _i32),
+        ("sm_scale", _f32),
+        ("qk_bias", _vp),
+        ("groups", _i64),
+        ("q_group", _i32),
+        ("out", _vp), ("out_dtype", _i32),
+        ("out_row_map", _vp),
+    ]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     "lbfq_last_error": (ctypes.c_char_p, []),
@@ -147,6 +173,8 @@ _SIGS = {
     "lbfq_blasst_scan": (_i32, [_vp, _vp, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp]),
     "lbfq_blasst_keep": (_i32, [_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp]),
     "lbfq_blasst_attend": (_i32, [ctypes.POINTER(BlasstAttendParams), _vp]),
+    "lbfq_sdpa_dequant": (_i32, [ctypes.POINTER(SdpaDequantParams), _vp]),
+    "lbfq_sdpa_fwd": (_i32, [ctypes.POINTER(SdpaParams), _vp]),
     "lbfq_hbm_stream": (_i32, [_i32, _vp, _vp, _i64, _i32, _vp, _vp]),
     "lbfq_issue_probe": (_i32, [_i32, _i32, _i32, _vp, _vp, _vp]),
     "lbfq_selftest_cvt_fp8": (_i32, [_vp, _i64, _vp, _vp]),

@@ -18,39 +18,28 @@ Execution differs from the reference in how the work is laid out:
   the qm_k row-max estimate come from one qm.K_s pass, and one FP8-MFMA kernel
   computes attention, writing rows directly to their original (pre-k-means)
   positions of the NHD output.
-* SDPA path (``attention.py:247-321``): quant/dequant on the HIP kernels, then
-  the attention in fp32 torch on the GPU with contiguous operands.
+* SDPA path (``attention.py:245-321``): the same prepass quantisers, a
+  dequantisation into the SDPA dtype (V transposed, V block means added), and
+  one bf16/fp16-MFMA flash-attention kernel with P not quantised, writing rows
+  directly to their original positions.
 """
 
 from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import Optional, Tuple
+from typing import Optional
 
 import torch
 
 from . import _lib
 from ._ops import RowSource, channel_amax, colsum_mean, column_mean, hadamard_scale, qmk, round_up, rowtile
-from .attention_kernel import launch_attention, parse_blasst_fill, v_tile_colsum, validate_kernel_config
+from .attention_kernel import launch_attention, v_tile_colsum, validate_kernel_config
 from .config import QuantConfig
-from .hadamard import apply_qk_hadamard, qk_signs_device
-from .kmeans import KMeansReorderResult, gather_rows, kmeans_labels, make_result
+from .hadamard import qk_signs_device
+from .kmeans import KMeansReorderResult, kmeans_labels, make_result
+
 LOG2E = 1.4426950408889634
-
-from .quant import (
-    fp8_block_dequant,
-    fp8_block_quant,
-    fp8_per_channel_dequant,
-    fp8_per_channel_quant,
-    mxfp8_qk_dequant,
-    mxfp8_qk_quant,
-    mxfp8_v_dequant,
-    mxfp8_v_quant,
-)
-
-_FP8_E4M3_MAX = 448.0
-_LOG2_E = 1.4426950408889634
 
 
 @dataclass
@@ -331,7 +320,7 @@ def _p_requant_hip(prep: _Prep, cfg: QuantConfig, sm_scale: float, out_dtype: to
 
 
 # ---------------------------------------------------------------------------
-# Path A: dequant Q/K/V -> attention with fp32 P (reference attention.py:247-321)
+# Path A: dequant Q/K/V -> attention with P not quantised (reference attention.py:245-321)
 # ---------------------------------------------------------------------------
 
 
@@ -344,104 +333,95 @@ def _k_quant_fusable(k: RowSource, cfg: QuantConfig, P: int, groups: int) -> boo
             and k.sub_mode in (_lib.SUB_NONE, _lib.SUB_COLVEC) and groups * P * 4 < (1 << 32))
 
 
-def _qk_inputs_for_quant(q_work, k_work, cfg):
-    if not cfg.qk_hadamard:
-        return q_work, k_work
-    return apply_qk_hadamard(q_work, k_work, random_sign=cfg.qk_hadamard_random_sign, seed=cfg.qk_hadamard_seed)
+@dataclass
+class SdpaOperands:
+    """Path A's operands in the SDPA dtype, head-major, S padded to the pitch P
+    with zeros, plus the qm correction table."""
+
+    b: int
+    s: int
+    h: int
+    d: int
+    P: int
+    q: torch.Tensor                       # (B,H,P,D) sdpa dtype
+    k: torch.Tensor                       # (B,H,P,D)
+    v_t: torch.Tensor                     # (B,H,D,P), V block means added
+    bias: Optional[torch.Tensor]          # (B,H,G,P) qm.K_s * sm_scale * log2(e)
+    q_group: int
+    out_row_map: Optional[torch.Tensor]   # (B*H,S) int32
 
 
-def _quant_qk(t, cfg):
-    if cfg.qk_quant == "fp8_block":
-        q, s = fp8_block_quant(t, block_s=cfg.fp8_block_size)
-        return q, s, {"kind": "fp8_block", "block_s": cfg.fp8_block_size}
-    if cfg.qk_quant == "mxfp8":
-        q, s = mxfp8_qk_quant(t, block_d=cfg.mxfp8_block_size)
-        return q, s, {"kind": "mxfp8", "block_d": cfg.mxfp8_block_size}
-    raise ValueError(f"unsupported qk_quant: {cfg.qk_quant!r}")
+def sdpa_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float, sdpa_dtype: torch.dtype) -> SdpaOperands:
+    """Quantise Q/K/V with the reference's quantisers (attention.py:271-273: the
+    same codes as the P-requant path's prepass), dequantise them into the SDPA
+    dtype and add the V block means (attention.py:274-286), and form the qm
+    correction of the Q-smoothing branch (attention.py:311-312)."""
+    b, s, h, d = prep.q.shape
+    dev = prep.q.x.device
+    P = round_up(s, 128)
+    signs = None
+    if cfg.qk_hadamard and cfg.qk_hadamard_random_sign:
+        signs = qk_signs_device(h, d, cfg.qk_hadamard_seed, dev)
+    q_codes, q_scale = _quant_qk_codes(prep.q, cfg, P, signs=signs)
+    k_codes, k_scale = _quant_qk_codes(prep.k, cfg, P, signs=signs)
+    v_codes, v_scale, v_kind, v_block = _quant_v_codes(prep.v, cfg, P)
+    v_alpha = None
+    if prep.v_alpha is not None:
+        if s % cfg.v_smooth_block_size != 0:
+            raise ValueError(f"S={s} not divisible by v_smooth_block_size={cfg.v_smooth_block_size}")
+        v_alpha = prep.v_alpha.permute(0, 2, 1, 3).float().contiguous()
+    q_deq = torch.empty((b, h, P, d), dtype=sdpa_dtype, device=dev)
+    k_deq = torch.empty_like(q_deq)
+    v_t = torch.empty((b, h, d, P), dtype=sdpa_dtype, device=dev)
+    mx = cfg.qk_quant == "mxfp8"
+    p = _lib.SdpaDequantParams(
+        B=b, H=h, S=s, D=d, s_pitch=P, q_codes=q_codes.data_ptr(), k_codes=k_codes.data_ptr(),
+        v_codes_t=v_codes.data_ptr(), qk_mx=int(mx), q_scale=q_scale.data_ptr(), k_scale=k_scale.data_ptr(),
+        qk_block=cfg.mxfp8_block_size if mx else cfg.fp8_block_size, v_kind=v_kind, v_scale=v_scale.data_ptr(),
+        v_block=v_block, v_alpha=_lib.ptr(v_alpha), v_smooth_block=cfg.v_smooth_block_size if v_alpha is not None
+        else 0, sdpa_dtype=_lib.DTYPE_CODE[sdpa_dtype], q_out=q_deq.data_ptr(), k_out=k_deq.data_ptr(),
+        v_t_out=v_t.data_ptr())
+    _lib.check(_lib.load().lbfq_sdpa_dequant(p, _lib.stream_handle(dev)), "lbfq_sdpa_dequant")
+    bias = None
+    if prep.qm is not None:
+        bias, _ = qmk(prep.qm, prep.k, sm_scale * LOG2E, s_pitch=P, want_rowmax=False)
+    return SdpaOperands(b=b, s=s, h=h, d=d, P=P, q=q_deq, k=k_deq, v_t=v_t, bias=bias,
+                        q_group=cfg.q_smooth_block_size, out_row_map=prep.q_order_i32())
 
 
-def _dequant_qk(fp8, scale, meta, dtype):
-    if meta["kind"] == "fp8_block":
-        return fp8_block_dequant(fp8, scale, block_s=meta["block_s"], dtype=dtype)
-    if meta["kind"] == "mxfp8":
-        return mxfp8_qk_dequant(fp8, scale, block_d=meta["block_d"], dtype=dtype)
-    raise ValueError(f"bad meta: {meta!r}")
-
-
-def _quant_v(t, cfg):
-    if cfg.v_quant == "fp8_channel":
-        q, s = fp8_per_channel_quant(t)
-        return q, s, {"kind": "fp8_channel"}
-    if cfg.v_quant == "fp8_block":
-        q, s = fp8_block_quant(t, block_s=cfg.v_fp8_block_size)
-        return q, s, {"kind": "fp8_block", "block_s": cfg.v_fp8_block_size}
-    if cfg.v_quant == "mxfp8":
-        q, s = mxfp8_v_quant(t, block_s=cfg.v_mxfp8_block_size)
-        return q, s, {"kind": "mxfp8", "block_s": cfg.v_mxfp8_block_size}
-    raise ValueError(f"unsupported v_quant: {cfg.v_quant!r}")
-
-
-def _dequant_v(fp8, scale, meta, dtype):
-    if meta["kind"] == "fp8_channel":
-        return fp8_per_channel_dequant(fp8, scale, dtype=dtype)
-    if meta["kind"] == "fp8_block":
-        return fp8_block_dequant(fp8, scale, block_s=meta["block_s"], dtype=dtype)
-    if meta["kind"] == "mxfp8":
-        return mxfp8_v_dequant(fp8, scale, block_s=meta["block_s"], dtype=dtype)
-    raise ValueError(f"bad meta: {meta!r}")
-
-
-def _attention_fp32(qb, kb, vb, sm_scale, *, corr_q=None, corr_k=None, group=None, chunk=512, p_dtype=None):
-    """softmax(q k^T * scale [+ corr]) v over BHSD tensors in fp32 with contiguous
-    operands, chunked over queries (bounded memory).  ``p_dtype`` rounds the
-    main scores (before the scale and the correction) and the probabilities
-    before the PV product to the SDPA dtype, as the reference's chunked path
-    does (attention.py:314, 318)."""
-    B, H, S, D = qb.shape
-    kT = kb.float().transpose(-2, -1).contiguous()
-    vf = vb.float().contiguous()
-    ksT = corr_k.float().transpose(-2, -1).contiguous() if corr_k is not None else None
-    out = torch.empty((B, H, S, D), dtype=torch.float32, device=qb.device)
-    grp_idx = torch.arange(S, device=qb.device) // group if group else None
-    for m0 in range(0, S, chunk):
-        m1 = min(m0 + chunk, S)
-        scores = torch.matmul(qb[:, :, m0:m1].float().contiguous(), kT)
-        if p_dtype is not None:
-            # the reference's main term is a matmul of the sdpa-dtype operands,
-            # whose output is in that dtype (attention.py:314)
-            scores = scores.to(p_dtype).float()
-        scores = scores * sm_scale
-        if corr_q is not None:
-            scores = scores + torch.matmul(corr_q[:, :, grp_idx[m0:m1]].float().contiguous(), ksT) * sm_scale
-        p = torch.softmax(scores, dim=-1)
-        if p_dtype is not None:
-            p = p.to(p_dtype).float()
-        out[:, :, m0:m1] = torch.matmul(p, vf)
+def launch_sdpa(ops: SdpaOperands, sm_scale: float, out_dtype: torch.dtype) -> torch.Tensor:
+    """The attention of path A (attention.py:288-319) on the dequantised operands:
+    NHD output in ``out_dtype`` (values rounded to the SDPA dtype), rows in
+    their original (pre-k-means) positions."""
+    dev = ops.q.device
+    out = torch.empty((ops.b, ops.s, ops.h, ops.d), dtype=out_dtype, device=dev)
+    p = _lib.SdpaParams(
+        B=ops.b, H=ops.h, S=ops.s, D=ops.d, s_pitch=ops.P, q=ops.q.data_ptr(), k=ops.k.data_ptr(),
+        v_t=ops.v_t.data_ptr(), sdpa_dtype=_lib.DTYPE_CODE[ops.q.dtype], sm_scale=float(sm_scale),
+        qk_bias=_lib.ptr(ops.bias), groups=ops.bias.shape[2] if ops.bias is not None else 0,
+        q_group=ops.q_group if ops.bias is not None else 0, out=out.data_ptr(), out_dtype=_lib.DTYPE_CODE[out_dtype],
+        out_row_map=_lib.ptr(ops.out_row_map))
+    _lib.check(_lib.load().lbfq_sdpa_fwd(p, _lib.stream_handle(dev)), "lbfq_sdpa_fwd")
     return out
 
 
-def _fake_quant_attention_sdpa(q_work, k_work, v_work, qm, v_alpha, cfg, sm_scale, sdpa_dtype):
-    b, s, h, d = q_work.shape
-    q_in, k_in = _qk_inputs_for_quant(q_work, k_work, cfg)
-    q_fp8, q_scale, q_meta = _quant_qk(q_in, cfg)
-    k_fp8, k_scale, k_meta = _quant_qk(k_in, cfg)
-    v_fp8, v_scale, v_meta = _quant_v(v_work, cfg)
-    q_deq = _dequant_qk(q_fp8, q_scale, q_meta, sdpa_dtype)
-    k_deq = _dequant_qk(k_fp8, k_scale, k_meta, sdpa_dtype)
-    v_deq = _dequant_v(v_fp8, v_scale, v_meta, sdpa_dtype)
-    if v_alpha is not None:
-        block_v = cfg.v_smooth_block_size
-        if s % block_v != 0:
-            raise ValueError(f"S={s} not divisible by v_smooth_block_size={block_v}")
-        v_deq = v_deq + v_alpha.repeat_interleave(block_v, dim=1).to(sdpa_dtype)
-    perm = (0, 2, 1, 3)
-    qb, kb, vb = (t.permute(*perm) for t in (q_deq, k_deq, v_deq))
-    if qm is None:
-        o = _attention_fp32(qb, kb, vb, sm_scale).to(sdpa_dtype)
-    else:
-        o = _attention_fp32(qb, kb, vb, sm_scale, corr_q=qm.permute(*perm), corr_k=k_work.permute(*perm),
-                            group=cfg.q_smooth_block_size, p_dtype=sdpa_dtype).to(sdpa_dtype)
-    return o.permute(*perm).contiguous()
+def _sdpa_hip(prep: _Prep, cfg: QuantConfig, sm_scale: float, out_dtype: torch.dtype,
+              sdpa_dtype: torch.dtype) -> torch.Tensor:
+    return launch_sdpa(sdpa_operands(prep, cfg, sm_scale, sdpa_dtype), sm_scale, out_dtype)
+
+
+def _attention_fp32(qb, kb, vb, sm_scale, *, chunk=512):
+    """softmax(q k^T * scale) v over BHSD tensors in fp32 with contiguous
+    operands, chunked over queries (bounded memory)."""
+    B, H, S, D = qb.shape
+    kT = kb.float().transpose(-2, -1).contiguous()
+    vf = vb.float().contiguous()
+    out = torch.empty((B, H, S, D), dtype=torch.float32, device=qb.device)
+    for m0 in range(0, S, chunk):
+        m1 = min(m0 + chunk, S)
+        scores = torch.matmul(qb[:, :, m0:m1].float().contiguous(), kT) * sm_scale
+        out[:, :, m0:m1] = torch.matmul(torch.softmax(scores, dim=-1), vf)
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -517,11 +497,7 @@ def fake_quant_attention(
     if cfg.p_requant:
         o = _p_requant_hip(prep, cfg, sm_scale, out_dtype)
     else:
-        o = _fake_quant_attention_sdpa(prep.work("q"), prep.work("k"), prep.work("v"), prep.qm, prep.v_alpha, cfg,
-                                       sm_scale, sdpa_dtype).to(out_dtype)
-        inv = prep.q_inverse_i32()
-        if inv is not None:
-            o = gather_rows(o, inv)
+        o = _sdpa_hip(prep, cfg, sm_scale, out_dtype, sdpa_dtype)
 
     if return_artifacts:
         km = prep.q_km_result if prep.q_km_result is not None else _kmeans_result(q.contiguous(), prep.q_km)

@@ -35,6 +35,11 @@ The attention kernel is checked in three parts, each against the CPU oracle
    comes from the scores.  BLASST decisions must agree with the reference
    except in rows whose predicate margin is within the score perturbation of
    ln(lambda).
+4. **Path A** (``p_requant=False``): ``sdpa_replay`` evaluates the
+   reference's SDPA / Q-smoothing attention in float64 on the native path's
+   own dequantised operands and bounds the difference element-wise by one
+   SDPA-dtype ulp plus the roundings the kernel's fp32 arithmetic may resolve
+   the other way.
 """
 
 from __future__ import annotations
@@ -323,8 +328,89 @@ def unpermute_rows(t: torch.Tensor, order) -> torch.Tensor:
     return o
 
 
+def ulp_dt(x: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+    """One ulp of the SDPA dtype (bf16: 8 significant bits, fp16: 11) at |x|;
+    the spacing of the smallest normal binade below it."""
+    bits, tiny = (7, 2.0 ** -126) if dt == torch.bfloat16 else (10, 2.0 ** -14)
+    return torch.pow(2.0, torch.floor(torch.log2(x.abs().double().clamp_min(tiny))) - bits)
+
+
+def _rnd(x: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+    """x rounded to fp32, then to dt (the kernel rounds fp32 values)."""
+    return x.float().to(dt).double()
+
+
+def sdpa_replay(sops, out: torch.Tensor, sm_scale: float, rows=None) -> dict:
+    """Path A's attention (attention.py:288-319) in float64 on the kernel's own
+    operands (``SdpaOperands``: Q, K, V^T in the SDPA dtype, the qm.K_s table),
+    against the kernel's output ``out`` (NHD, caller row order), optionally
+    for a subset of the kernel's query rows.
+
+    Element-wise, |out - o64| <= ulp(o64) + A.  The ulp covers the output's
+    rounding to the SDPA dtype; A is what the kernel's fp32 arithmetic may
+    legitimately move:
+
+    * no qm (SDPA, P in fp32): every score carries the fp32 accumulation error
+      D 2^-24 sum|q||k| (times sm_scale) and every P a relative error below
+      2^-15 (its two-term SDPA-dtype representation, exp2, the normalisation):
+      A = 2 max|v| sum_j p_j (e^delta_j - 1) + S 2^-24 p.|v|;
+    * qm branch: the main score is rounded to the SDPA dtype (attention.py:314)
+      and P is rounded after the normalisation (:318).  Where the float64 main
+      score lies within the fp32 accumulation error of a rounding boundary,
+      the kernel may round it one ulp the other way: those scores add
+      2 max|v| p_j (e^(ulp sm) - 1) to A, and they shift every other P of the
+      row by the same relative amount, which widens the window (2^-16
+      relative, plus that shift) inside which a P may round the other way,
+      adding ulp(p_i)|v_i| for each such P.
+
+    Returns the largest |diff| / bound ("excess", <= 1 passes), the fraction
+    of elements equal to the rounded float64 value, the largest |diff| and the
+    counts of boundary cases."""
+    dt = sops.q.dtype
+    b, h, s, d = sops.b, sops.h, sops.s, sops.d
+    ridx = torch.arange(s) if rows is None else torch.as_tensor(rows).long()
+    q = sops.q[:, :, :s].cpu().double()[:, :, ridx]
+    k = sops.k[:, :, :s].cpu().double()
+    v = sops.v_t[..., :s].cpu().double().transpose(-1, -2)                 # (B,H,S,D)
+    o = out.cpu().double().permute(0, 2, 1, 3)                              # output-row order
+    if sops.out_row_map is not None:
+        order = sops.out_row_map.cpu().long().reshape(b, h, s)
+        o = torch.gather(o, 2, order.unsqueeze(-1).expand(-1, -1, -1, d))  # kernel row order
+    o = o[:, :, ridx]
+    main = q @ k.transpose(-1, -2)
+    err_main = d * 2.0 ** -24 * (q.abs() @ k.abs().transpose(-1, -2))
+    vabs = v.abs()
+    vmax = vabs.amax(dim=2, keepdim=True)                                   # (B,H,1,D)
+    acc_err = s * 2.0 ** -24
+    info = {}
+    if sops.bias is None:
+        p = torch.softmax(main * sm_scale, dim=-1)
+        o64 = p @ v
+        delta = sm_scale * err_main + 2.0 ** -15
+        allow = 2 * vmax * (p * torch.expm1(delta)).sum(-1, keepdim=True) + acc_err * (p @ vabs)
+    else:
+        g = sops.bias.shape[2]
+        grp = (ridx // sops.q_group).clamp_max(g - 1)
+        bias = sops.bias.cpu().double()[:, :, grp, :s]
+        main_r = _rnd(main, dt)
+        amb_m = _rnd(main - err_main, dt) != _rnd(main + err_main, dt)
+        u = main_r * (sm_scale * LOG2E) + bias                              # log2 units
+        p = torch.softmax(u * math.log(2.0), dim=-1)
+        p_r = _rnd(p, dt)
+        shift = (amb_m * p * torch.expm1(ulp_dt(main, dt) * sm_scale)).sum(-1, keepdim=True)
+        rel = 2.0 ** -16 + shift
+        amb_p = _rnd(p * (1 - rel), dt) != _rnd(p * (1 + rel), dt)
+        o64 = p_r @ v
+        allow = 2 * vmax * shift + (amb_p * ulp_dt(p, dt)) @ vabs + acc_err * (p_r @ vabs)
+        info = dict(frac_main_boundary=amb_m.double().mean().item(), frac_p_boundary=amb_p.double().mean().item())
+    bound = ulp_dt(o64, dt) + allow
+    diff = (o - o64).abs()
+    return dict(excess=(diff / bound).max().item(), frac_equal=(o == _rnd(o64, dt)).double().mean().item(),
+                max_abs=diff.max().item(), **info)
+
+
 __all__ = ["COS_MIN", "MAXABS", "MFMA_REL", "cosine", "ulp_bf16", "tolerance", "kernel_operands", "kernel_scores",
            "replay", "strict_check", "check_against_replay", "angle", "reference_bound",
            "exact_scores_and_bound", "flipped_codes",
            "skip_agreement", "sampled_rows", "gather_caller_rows", "unpermute_rows",
-           "math"]
+           "ulp_dt", "sdpa_replay", "math"]

@@ -33,7 +33,8 @@ def test_struct_layouts_match_header():
     """ctypes structs mirror the C structs field by field (names, order)."""
     from low_bit_fake_quant import _lib
     text = open(os.path.join(REPO, "include", "lbfq.h")).read()
-    for struct, cls in (("lbfq_rowtile_params", _lib.RowTileParams), ("lbfq_attn_params", _lib.AttnParams)):
+    for struct, cls in (("lbfq_rowtile_params", _lib.RowTileParams), ("lbfq_attn_params", _lib.AttnParams),
+                        ("lbfq_sdpa_dequant_params", _lib.SdpaDequantParams), ("lbfq_sdpa_params", _lib.SdpaParams)):
         body = re.search(r"typedef struct \{((?:(?!typedef struct).)*?)\}\s*" + struct, text, flags=re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         names = []
