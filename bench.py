@@ -41,6 +41,7 @@ import torch  # noqa: E402
 FP8_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 MFMA (datasheet)
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3   # MI355X fp32 (vector / MFMA, dense)
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (datasheet)
 
 
 def log(msg: str) -> None:
@@ -289,6 +290,50 @@ def other_configs(configs, dev, steps: int = 5, err_rows: int = 1024):
         res[str(c)] = r
         del out, q, k, v
         torch.cuda.empty_cache()
+    return res
+
+
+def path_a(dev, steps: int = 5):
+    """The reference's path A (``p_requant=False``) on its native kernels: config
+    0 end to end (timed, and its whole output against the oracle), and the
+    attention kernel alone at config 1's shape with P not quantised (dense-
+    equivalent 4 N^2 D H flops against the bf16 MFMA peak)."""
+    from low_bit_fake_quant import fake_quant_attention
+    from low_bit_fake_quant.attention import _lazy_preprocess, launch_sdpa, sdpa_operands
+    from low_bit_fake_quant.wan import make_inputs, pad_qkv, workloads
+    res = {}
+    w = workloads()[0]
+    q, k, v = make_inputs(w, seed=0)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    ms0 = _events_time(lambda: fake_quant_attention(qd, kd, vd, w.cfg), 20, 3)
+    out = fake_quant_attention(qd, kd, vd, w.cfg).cpu()
+    r0 = {"workload": w.name, "e2e_ms": ms0}
+    try:
+        from oracle import pipeline as opipe
+        r0["err_vs_oracle"] = _err(out, opipe.fake_quant_attention(q, k, v, w.cfg))
+        r0["err_vs_oracle"]["rows"] = "all"
+    except Exception as e:  # report, do not lose the timing
+        r0["err_vs_oracle"] = {"error": repr(e)}
+    res["config0"] = r0
+    log(f"path A config 0: {ms0:.3f} ms, err {r0['err_vs_oracle']}")
+    w1 = workloads()[1]
+    cfg = dataclasses.replace(w1.cfg, p_requant=False)
+    q, k, v = make_inputs(w1, seed=0)
+    q, k, v, n = pad_qkv(q, k, v, cfg)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    sm = 1.0 / (w1.D ** 0.5)
+    prep = _lazy_preprocess(qd, kd, vd, cfg)
+    ops_ms = _events_time(lambda: sdpa_operands(prep, cfg, sm, torch.bfloat16), steps, 1)
+    sops = sdpa_operands(prep, cfg, sm, torch.bfloat16)
+    ms = _events_time(lambda: launch_sdpa(sops, sm, torch.bfloat16), steps, 1)
+    fl = 4.0 * n * n * w1.D * w1.H
+    res["config1_shape"] = {"workload": w1.name + " with p_requant=False", "attention_ms": ms,
+                            "quantise_dequantise_ms": ops_ms, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+                            "frac_of_bf16_peak": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                            "note": "bf16 MFMA, P unquantised (two PV products: P's bf16 rounding and residual)"}
+    log(f"path A at config 1's shape: {ms:.3f} ms, {res['config1_shape']['TFLOPs']:.1f} TFLOP/s")
+    del sops, prep, qd, kd, vd
+    torch.cuda.empty_cache()
     return res
 
 
@@ -639,6 +684,7 @@ def main() -> int:
         del qd, kd, vd, ops, prep
         torch.cuda.empty_cache()
         others = other_configs([1, 3, 4], dev)
+        others["path_a"] = path_a(dev)
 
     roof = {"bound": "mfma", "achieved": tflops, "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": tflops / FP8_PEAK_TFLOPS, "traffic": None,

@@ -41,6 +41,8 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -106,17 +108,74 @@ struct SdpaArgs {
   const int32_t* out_row_map;
 };
 
-// S^T of the 64 keys from key0 for the lane's query: two 32-key blocks
+// LDS staging of one 64-key tile, shared by the workgroup's four waves and
+// double-buffered: the K rows (D bf16 each, pitch KP bytes) and the V^T rows
+// (64 keys each, pitch VP bytes).  The pitches are 16 bytes past a multiple of
+// 128 so that the eight rows one ds_read_b128 phase touches fall on distinct
+// banks.  Within each 16-key group the V^T keys are stored in the order
+// 0-3, 8-11, 4-7, 12-15: lane group g's eight k-elements of a PV k-step are
+// then one contiguous 16-byte read.
+template <int D>
+struct Stage {
+  static constexpr int KP = 2 * D + 16;
+  static constexpr int VP = 2 * 64 + 16;
+  static constexpr int KBYTES = 64 * KP;
+  static constexpr int BUF = KBYTES + D * VP;
+  static constexpr int KCH = 64 * D / 8 / 256;  // 16-byte K chunks per thread
+  static constexpr int VCH = D * 8 / 256;       // 16-byte V^T chunks per thread
+};
+
+// global -> registers: the thread's K and V^T chunks of the tile at key0
+template <int D, bool WITH_V>
+__device__ __forceinline__ void stage_load(const uint16_t* kbase, const uint16_t* vbase, int P, int key0, int tid,
+                                           u32x4 (&kr)[Stage<D>::KCH], u32x4 (&vr)[Stage<D>::VCH]) {
+  constexpr int CPR = D / 8;  // K chunks per row
+#pragma unroll
+  for (int i = 0; i < Stage<D>::KCH; ++i) {
+    const int c = tid + 256 * i, row = c / CPR, col = c % CPR;
+    kr[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<size_t>(key0 + row) * D + 8 * col);
+  }
+  if constexpr (WITH_V) {
+#pragma unroll
+    for (int i = 0; i < Stage<D>::VCH; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      vr[i] = *reinterpret_cast<const u32x4*>(vbase + static_cast<size_t>(row) * P + key0 + 8 * kc);
+    }
+  }
+}
+
+// registers -> LDS buffer (the key permutation of V^T applied here)
+template <int D, bool WITH_V>
+__device__ __forceinline__ void stage_store(uint8_t* buf, int tid, const u32x4 (&kr)[Stage<D>::KCH],
+                                            const u32x4 (&vr)[Stage<D>::VCH]) {
+  constexpr int CPR = D / 8;
+#pragma unroll
+  for (int i = 0; i < Stage<D>::KCH; ++i) {
+    const int c = tid + 256 * i, row = c / CPR, col = c % CPR;
+    *reinterpret_cast<u32x4*>(buf + row * Stage<D>::KP + 16 * col) = kr[i];
+  }
+  if constexpr (WITH_V) {
+#pragma unroll
+    for (int i = 0; i < Stage<D>::VCH; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      // keys 16 G + 8 h + [0,4) -> positions 16 G + 4 h + [0,4); + [4,8) -> 16 G + 8 + 4 h + [0,4)
+      uint8_t* rp = buf + Stage<D>::KBYTES + row * Stage<D>::VP + 2 * (16 * (kc >> 1) + 4 * (kc & 1));
+      *reinterpret_cast<u32x2*>(rp) = vr[i].xy;
+      *reinterpret_cast<u32x2*>(rp + 16) = vr[i].zw;
+    }
+  }
+}
+
+// S^T of the staged tile for the lane's query: two 32-key blocks
 template <int D, int DT>
-__device__ __forceinline__ void scores(const uint16_t* kbase, int key0, int li, int g, const uint4 (&qop)[D / 16],
-                                       v16f (&s)[2]) {
+__device__ __forceinline__ void scores(const uint8_t* buf, int li, int g, const uint4 (&qop)[D / 16], v16f (&s)[2]) {
   constexpr int NKS = D / 16;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    const uint16_t* krow = kbase + static_cast<size_t>(key0 + 32 * kb + li) * D + 8 * g;
+    const uint8_t* krow = buf + (32 * kb + li) * Stage<D>::KP + 16 * g;
     uint4 kop[NKS];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) kop[ks] = *reinterpret_cast<const uint4*>(krow + 16 * ks);
+    for (int ks = 0; ks < NKS; ++ks) kop[ks] = *reinterpret_cast<const uint4*>(krow + 32 * ks);
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
 #pragma unroll
@@ -125,20 +184,35 @@ __device__ __forceinline__ void scores(const uint16_t* kbase, int key0, int li, 
 }
 
 // log2-unit scores of the lane's 32 keys (register r of block kb is key
-// key0 + 32 kb + 8 (r / 4) + 4 g + r % 4), keys >= S set to -inf
+// key0 + 32 kb + 8 (r / 4) + 4 g + r % 4); in the tile that holds key S - 1,
+// keys >= S are set to -inf
 template <bool BIAS, int DT>
 __device__ __forceinline__ void to_log2(const v16f (&s)[2], int key0, int g, int S, float sml2, const float* brow,
                                         float (&u)[32]) {
+  if constexpr (BIAS) {
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = key0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
-      float x;
-      if constexpr (BIAS) x = fmaf(round_dt<DT>(s[kb][r]), sml2, brow[key]);  // main term rounded to DT first
-      else x = s[kb][r] * sml2;
-      u[16 * kb + r] = key < S ? x : -INFINITY;
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 bv = *reinterpret_cast<const float4*>(brow + key0 + 32 * kb + 8 * q4 + 4 * g);
+        const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)  // the main term rounded to DT first
+          u[16 * kb + 4 * q4 + e] = fmaf(round_dt<DT>(s[kb][4 * q4 + e]), sml2, bb[e]);
+      }
     }
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) u[16 * kb + r] = s[kb][r] * sml2;
+  }
+  if (key0 + 64 > S) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (key0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3) >= S) u[16 * kb + r] = -INFINITY;
   }
 }
 
@@ -157,38 +231,39 @@ __device__ __forceinline__ void pack(const float (&p)[32], uint32_t (&w)[2][2][4
       }
 }
 
-// O^T (D x 32 queries) += V^T (D x 64 keys) P^T for the tile at key0
+// O^T (D x 32 queries) += V^T (D x 64 keys) P^T for the staged tile
 template <int D, int DT>
-__device__ __forceinline__ void pv(const uint16_t* vbase, int P, int key0, int li, int g, const uint32_t (&w)[2][2][4],
+__device__ __forceinline__ void pv(const uint8_t* buf, int li, int g, const uint32_t (&w)[2][2][4],
                                    v16f (&acc)[D / 32]) {
+  const uint8_t* vb = buf + Stage<D>::KBYTES + li * Stage<D>::VP + 16 * g;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const uint4 pb = make_uint4(w[kb][j][0], w[kb][j][1], w[kb][j][2], w[kb][j][3]);
-      const int kv = key0 + 32 * kb + 16 * j + 4 * g;
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) {
-        const uint16_t* vrow = vbase + static_cast<size_t>(32 * db + li) * P + kv;
-        const uint2 x = *reinterpret_cast<const uint2*>(vrow);
-        const uint2 y = *reinterpret_cast<const uint2*>(vrow + 8);
-        acc[db] = mfma16<DT>(make_uint4(x.x, x.y, y.x, y.y), pb, acc[db]);
+        const uint4 va = *reinterpret_cast<const uint4*>(vb + 32 * db * Stage<D>::VP + 32 * (2 * kb + j));
+        acc[db] = mfma16<DT>(va, pb, acc[db]);
       }
     }
   }
 }
 
 template <int D, bool BIAS, int DT>
-__global__ void __launch_bounds__(256) sdpa_fwd_kernel(const SdpaArgs a) {
+__global__ void __launch_bounds__(256, 2) sdpa_fwd_kernel(const SdpaArgs a) {
   constexpr int NKS = D / 16, NDB = D / 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  using St = Stage<D>;
+  __shared__ __align__(16) uint8_t lds[2 * St::BUF];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, g = lane >> 5;
   const int nqb = a.P / 128;
   const int bh = blockIdx.x / nqb, qb = blockIdx.x - bh * nqb;
-  const int q0 = qb * 128 + wave * 32;
-  if (q0 >= a.S) return;  // wave-uniform: a wave of padding rows only (no barriers in this kernel)
   const int S = a.S, P = a.P;
-  const int qi = q0 + li;  // < P: rows [S, P) of q are zero
+  // every wave takes part in the staging and the barriers; a wave whose rows
+  // are all padding (rows [S, P) of q are zero) computes and stores nothing
+  const int qi = qb * 128 + wave * 32 + li;
 
   uint4 qop[NKS];
   {
@@ -205,6 +280,7 @@ __global__ void __launch_bounds__(256) sdpa_fwd_kernel(const SdpaArgs a) {
   const uint16_t* kbase = a.k + static_cast<size_t>(bh) * P * D;
   const uint16_t* vbase = a.v_t + static_cast<size_t>(bh) * D * P;
   const int nt = (S + 63) / 64;
+  u32x4 kr[St::KCH], vr[St::VCH];
 
   v16f acc[NDB];
 #pragma unroll
@@ -216,9 +292,14 @@ __global__ void __launch_bounds__(256) sdpa_fwd_kernel(const SdpaArgs a) {
   if constexpr (BIAS) {
     // pass 1: the row's max and sum (each lane over its own keys, merged at the end)
     float m = -INFINITY, l = 0.0f;
+    stage_load<D, false>(kbase, vbase, P, 0, tid, kr, vr);
+    stage_store<D, false>(lds, tid, kr, vr);
+    __syncthreads();
     for (int t = 0; t < nt; ++t) {
+      const uint8_t* buf = lds + (t & 1) * St::BUF;
       v16f s[2];
-      scores<D, DT>(kbase, 64 * t, li, g, qop, s);
+      scores<D, DT>(buf, li, g, qop, s);
+      stage_load<D, false>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
       float u[32];
       to_log2<true, DT>(s, 64 * t, g, S, a.sml2, brow, u);
       float tmax = u[0];
@@ -228,43 +309,57 @@ __global__ void __launch_bounds__(256) sdpa_fwd_kernel(const SdpaArgs a) {
       const float ms = m_new == -INFINITY ? 0.0f : m_new;  // a lane whose keys so far are all masked
       float sum = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 32; ++j) sum += exp2f(u[j] - ms);
-      l = l * exp2f(m - ms) + sum;
+      for (int j = 0; j < 32; ++j) sum += __builtin_amdgcn_exp2f(u[j] - ms);
+      l = l * __builtin_amdgcn_exp2f(m - ms) + sum;
       m = m_new;
+      stage_store<D, false>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
+      __syncthreads();
     }
     const float mo = __shfl_xor(m, 32, 64), lo = __shfl_xor(l, 32, 64);
     const float mrow = fmaxf(m, mo);  // finite: key 0 is valid
-    const float inv = 1.0f / (l * exp2f(m - mrow) + lo * exp2f(mo - mrow));
+    const float inv = 1.0f / (l * __builtin_amdgcn_exp2f(m - mrow) + lo * __builtin_amdgcn_exp2f(mo - mrow));
     // pass 2: P = dtype(exp2(u - max) / sum), O = P V
+    stage_load<D, true>(kbase, vbase, P, 0, tid, kr, vr);
+    stage_store<D, true>(lds, tid, kr, vr);
+    __syncthreads();
     for (int t = 0; t < nt; ++t) {
+      const uint8_t* buf = lds + (t & 1) * St::BUF;
       v16f s[2];
-      scores<D, DT>(kbase, 64 * t, li, g, qop, s);
+      scores<D, DT>(buf, li, g, qop, s);
+      stage_load<D, true>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
       float u[32];
       to_log2<true, DT>(s, 64 * t, g, S, a.sml2, brow, u);
 #pragma unroll
-      for (int j = 0; j < 32; ++j) u[j] = exp2f(u[j] - mrow) * inv;
+      for (int j = 0; j < 32; ++j) u[j] = __builtin_amdgcn_exp2f(u[j] - mrow) * inv;
       uint32_t w[2][2][4];
       pack<DT>(u, w);
-      pv<D, DT>(vbase, P, 64 * t, li, g, w, acc);
+      pv<D, DT>(buf, li, g, w, acc);
+      stage_store<D, true>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
+      __syncthreads();
     }
   } else {
     // online softmax; P as its SDPA-dtype rounding plus the rounded residual
     float m = -INFINITY, l = 0.0f;
+    stage_load<D, true>(kbase, vbase, P, 0, tid, kr, vr);
+    stage_store<D, true>(lds, tid, kr, vr);
+    __syncthreads();
     for (int t = 0; t < nt; ++t) {
+      const uint8_t* buf = lds + (t & 1) * St::BUF;
       v16f s[2];
-      scores<D, DT>(kbase, 64 * t, li, g, qop, s);
+      scores<D, DT>(buf, li, g, qop, s);
+      stage_load<D, true>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
       float u[32];
       to_log2<false, DT>(s, 64 * t, g, S, a.sml2, nullptr, u);
       float tmax = u[0];
 #pragma unroll
       for (int j = 1; j < 32; ++j) tmax = fmaxf(tmax, u[j]);
       const float m_new = fmaxf(m, xor32_max(tmax));  // finite: key 64 t is valid
-      const float alpha = exp2f(m - m_new);           // 0 on the first tile
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile
       m = m_new;
       float sum = 0.0f;
 #pragma unroll
       for (int j = 0; j < 32; ++j) {
-        u[j] = exp2f(u[j] - m_new);
+        u[j] = __builtin_amdgcn_exp2f(u[j] - m_new);
         sum += u[j];
       }
       l = l * alpha + sum;
@@ -280,8 +375,10 @@ __global__ void __launch_bounds__(256) sdpa_fwd_kernel(const SdpaArgs a) {
 #pragma unroll
       for (int j = 0; j < 32; ++j) res[j] = u[j] - round_dt<DT>(u[j]);  // exact in fp32
       pack<DT>(res, wlo);
-      pv<D, DT>(vbase, P, 64 * t, li, g, whi, acc);
-      pv<D, DT>(vbase, P, 64 * t, li, g, wlo, acc);
+      pv<D, DT>(buf, li, g, whi, acc);
+      pv<D, DT>(buf, li, g, wlo, acc);
+      stage_store<D, true>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
+      __syncthreads();
     }
     inv_l = 1.0f / xor32_add(l);
   }
