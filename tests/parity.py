@@ -344,7 +344,8 @@ def sdpa_replay(sops, out: torch.Tensor, sm_scale: float, rows=None) -> dict:
     """Path A's attention (attention.py:288-319) in float64 on the kernel's own
     operands (``SdpaOperands``: Q, K, V^T in the SDPA dtype, the qm.K_s table),
     against the kernel's output ``out`` (NHD, caller row order), optionally
-    for a subset of the kernel's query rows.
+    for a subset of the kernel's query rows (one index vector for every head,
+    or a (B*H, R) set per head).
 
     Element-wise, |out - o64| <= ulp(o64) + A.  The ulp covers the output's
     rounding to the SDPA dtype; A is what the kernel's fp32 arithmetic may
@@ -352,15 +353,17 @@ def sdpa_replay(sops, out: torch.Tensor, sm_scale: float, rows=None) -> dict:
 
     * no qm (SDPA, P in fp32): every score carries the fp32 accumulation error
       D 2^-24 sum|q||k| (times sm_scale) and every P a relative error below
-      2^-15 (its two-term SDPA-dtype representation, exp2, the normalisation):
-      A = 2 max|v| sum_j p_j (e^delta_j - 1) + S 2^-24 p.|v|;
+      2^-15 (its two-term SDPA-dtype representation, exp2): A = 2 max|v|
+      sum_j p_j (e^delta_j - 1) + S 2^-24 p.|v| + eps_l |o|, with eps_l =
+      (S/64 + 64) 2^-24 the relative error of the row sum (about S/64
+      rescaled tile sums of 32 terms per lane);
     * qm branch: the main score is rounded to the SDPA dtype (attention.py:314)
       and P is rounded after the normalisation (:318).  Where the float64 main
       score lies within the fp32 accumulation error of a rounding boundary,
       the kernel may round it one ulp the other way: those scores add
       2 max|v| p_j (e^(ulp sm) - 1) to A, and they shift every other P of the
       row by the same relative amount, which widens the window (2^-16
-      relative, plus that shift) inside which a P may round the other way,
+      relative, plus eps_l, plus that shift) inside which a P may round the other way,
       adding ulp(p_i)|v_i| for each such P.
 
     Returns the largest |diff| / bound ("excess", <= 1 passes), the fraction
@@ -369,36 +372,44 @@ def sdpa_replay(sops, out: torch.Tensor, sm_scale: float, rows=None) -> dict:
     dt = sops.q.dtype
     b, h, s, d = sops.b, sops.h, sops.s, sops.d
     ridx = torch.arange(s) if rows is None else torch.as_tensor(rows).long()
-    q = sops.q[:, :, :s].cpu().double()[:, :, ridx]
+    # kernel rows per (b, h): one set for every head, or (B*H, R) sets
+    ridx = (ridx.expand(b * h, -1) if ridx.ndim == 1 else ridx).reshape(b, h, -1)
+
+    def take(t):  # (B,H,S,X) -> (B,H,R,X) at the kernel rows
+        return torch.gather(t, 2, ridx.unsqueeze(-1).expand(-1, -1, -1, t.shape[-1]))
+
+    q = take(sops.q[:, :, :s].cpu().double())
     k = sops.k[:, :, :s].cpu().double()
     v = sops.v_t[..., :s].cpu().double().transpose(-1, -2)                 # (B,H,S,D)
     o = out.cpu().double().permute(0, 2, 1, 3)                              # output-row order
     if sops.out_row_map is not None:
         order = sops.out_row_map.cpu().long().reshape(b, h, s)
         o = torch.gather(o, 2, order.unsqueeze(-1).expand(-1, -1, -1, d))  # kernel row order
-    o = o[:, :, ridx]
+    o = take(o)
     main = q @ k.transpose(-1, -2)
     err_main = d * 2.0 ** -24 * (q.abs() @ k.abs().transpose(-1, -2))
     vabs = v.abs()
     vmax = vabs.amax(dim=2, keepdim=True)                                   # (B,H,1,D)
     acc_err = s * 2.0 ** -24
+    # the row sum accumulates ~S/64 rescaled tile sums of 32 terms per lane
+    l_err = (s / 64 + 64) * 2.0 ** -24
     info = {}
     if sops.bias is None:
         p = torch.softmax(main * sm_scale, dim=-1)
         o64 = p @ v
         delta = sm_scale * err_main + 2.0 ** -15
-        allow = 2 * vmax * (p * torch.expm1(delta)).sum(-1, keepdim=True) + acc_err * (p @ vabs)
+        allow = 2 * vmax * (p * torch.expm1(delta)).sum(-1, keepdim=True) + acc_err * (p @ vabs) + l_err * o64.abs()
     else:
         g = sops.bias.shape[2]
-        grp = (ridx // sops.q_group).clamp_max(g - 1)
-        bias = sops.bias.cpu().double()[:, :, grp, :s]
+        grp = (ridx // sops.q_group).clamp_max(g - 1)                      # (B,H,R)
+        bias = torch.gather(sops.bias.cpu()[..., :s], 2, grp.unsqueeze(-1).expand(-1, -1, -1, s)).double()
         main_r = _rnd(main, dt)
         amb_m = _rnd(main - err_main, dt) != _rnd(main + err_main, dt)
         u = main_r * (sm_scale * LOG2E) + bias                              # log2 units
         p = torch.softmax(u * math.log(2.0), dim=-1)
         p_r = _rnd(p, dt)
         shift = (amb_m * p * torch.expm1(ulp_dt(main, dt) * sm_scale)).sum(-1, keepdim=True)
-        rel = 2.0 ** -16 + shift
+        rel = 2.0 ** -16 + l_err + shift
         amb_p = _rnd(p * (1 - rel), dt) != _rnd(p * (1 + rel), dt)
         o64 = p_r @ v
         allow = 2 * vmax * shift + (amb_p * ulp_dt(p, dt)) @ vabs + acc_err * (p_r @ vabs)
