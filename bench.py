@@ -264,7 +264,7 @@ def other_configs(configs, dev, steps: int = 5, err_rows: int = 1024):
                       "wave_tiles_some_skipped": wt[..., 1].sum().item() / wave_tiles,
                       "mfma_executed_fraction": 1.0 - 0.5 * w_all if elide else 1.0,
                       "mfma_executed_note": "of the dense schedule's 8 MFMAs per wave and tile, from the "
-                                            "kernel's wave-tile counters (rocprof SQ_INSTS_MFMA agrees)"})
+                                            "kernel's wave-tile counters (rocprof SQ_INSTS_VALU_MFMA_MOPS_F8 / 256 agrees)"})
             cd = dataclasses.replace(cfg, blasst_lambda=None)
             ms_d = _events_time(lambda: launch_attention(ops, cd, sm, torch.bfloat16), steps, 3)
             r["dense_same_shape"] = {"ms": ms_d, "TFLOPs": fl / (ms_d * 1e-3) / 1e12,
