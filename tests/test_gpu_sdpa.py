@@ -60,6 +60,16 @@ CASES = {
     "full_fp32_in_kmeans": (dict(qk_quant="fp8_block", fp8_block_size=32, v_quant="fp8_channel", smoothing="full",
                                  q_smooth_block_size=256, q_kmeans_k=16, v_smooth_mode="off"),
                             dict(n=1024, d=128, dtype=torch.float32, q_clusters=8)),
+    # fp16 inputs through the Hadamard rotation: the rotated value is the fp32
+    # product rounded to fp16 (the reference's two roundings), then quantised
+    "fp16_hadamard_mx_full": (dict(qk_quant="mxfp8", mxfp8_block_size=32, qk_hadamard=True, v_quant="mxfp8",
+                                   v_mxfp8_block_size=64, smoothing="full", q_smooth_block_size=128,
+                                   q_kmeans_k=None, v_smooth_mode="per_block", v_smooth_block_size=64),
+                              dict(n=640, d=128, dtype=torch.float16, v_bias=True)),
+    "fp16_hadamard_block_konly": (dict(qk_quant="fp8_block", fp8_block_size=64, qk_hadamard=True,
+                                       v_quant="fp8_channel", smoothing="k_only", q_kmeans_k=None,
+                                       v_smooth_mode="off"),
+                                  dict(n=512, d=64, dtype=torch.float16)),
 }
 
 
