@@ -496,6 +496,9 @@ def main() -> int:
     ap.add_argument("--trace-timed-only", action="store_true",
                     help="for rocprofv3 --kernel-trace: the prepass, then only the warmup and timed attention "
                          "launches of the headline (no end-to-end, hook, diagnostic or other-config calls)")
+    ap.add_argument("--path-a-only", action="store_true",
+                    help="only the p_requant=False leg (config 0 end to end, the attention at config 1's shape); "
+                         "one JSON line, for rocprofv3 --kernel-trace")
     ap.add_argument("--clock-sample", type=int, default=0, metavar="LAUNCHES",
                     help="run LAUNCHES attention launches back to back while sampling the shader clock with "
                          "rocm-smi; print the samples and the rate against the clock-scaled FP8 peak")
@@ -514,6 +517,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.hbm_ceiling:
         print(json.dumps({"hbm_stream": hbm_ceiling(dev), "bytes": 1 << 31}))
+        return 0
+    if args.path_a_only:
+        print(json.dumps({"path_a": path_a(dev)}))
         return 0
     w = workloads()[args.config]
     cfg = w.cfg

@@ -200,6 +200,9 @@ __device__ __forceinline__ void to_log2(const v16f (&s)[2], int key0, int g, int
         for (int e = 0; e < 4; ++e)  // the main term rounded to DT first
           u[16 * kb + 4 * q4 + e] = fmaf(round_dt<DT>(s[kb][4 * q4 + e]), sml2, bb[e]);
       }
+      // the second block's correction loads stay behind the first block's use
+      // (all eight in flight at once took the kernel past 256 VGPRs)
+      __builtin_amdgcn_sched_barrier(0);
     }
   } else {
 #pragma unroll
