@@ -505,7 +505,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU per process; --gpus N>1 is not supported "
-                          "(heads shard with no communication; see DESIGN.md)", "n_gpus": args.gpus}))
+                          "(the path shards by heads with no communication)", "n_gpus": args.gpus}))
         return 2
 
     from low_bit_fake_quant import _lib, fake_quant_attention, prepare_for_attention
