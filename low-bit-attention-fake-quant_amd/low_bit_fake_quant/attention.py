@@ -36,8 +36,18 @@ from . import _lib
 from ._ops import RowSource, channel_amax, colsum_mean, column_mean, hadamard_scale, qmk, round_up, rowtile
 from .attention_kernel import launch_attention, v_tile_colsum, validate_kernel_config
 from .config import QuantConfig
-from .hadamard import qk_signs_device
+from .hadamard import apply_qk_hadamard, qk_signs_device
 from .kmeans import KMeansReorderResult, kmeans_labels, make_result
+from .quant import (
+    fp8_block_dequant,
+    fp8_block_quant,
+    fp8_per_channel_dequant,
+    fp8_per_channel_quant,
+    mxfp8_qk_dequant,
+    mxfp8_qk_quant,
+    mxfp8_v_dequant,
+    mxfp8_v_quant,
+)
 
 LOG2E = 1.4426950408889634
 
@@ -331,6 +341,59 @@ def _k_quant_fusable(k: RowSource, cfg: QuantConfig, P: int, groups: int) -> boo
     return (cfg.qk_quant == "fp8_block" and not cfg.qk_hadamard and k.x.dtype == torch.bfloat16
             and cfg.fp8_block_size in (16, 32, 64) and s % cfg.fp8_block_size == 0
             and k.sub_mode in (_lib.SUB_NONE, _lib.SUB_COLVEC) and groups * P * 4 < (1 << 32))
+
+
+# Quantise / dequantise helpers of the reference's path A (attention.py:89-160),
+# kept under the same names because callers and the reference's own tests use
+# them (tests/test_qk_hadamard.py imports the Q/K ones): NHD tensors through the
+# HIP quantisers of quant.py.  The native path A above does not go through them.
+
+
+def _qk_inputs_for_quant(q_work, k_work, cfg):
+    if not cfg.qk_hadamard:
+        return q_work, k_work
+    return apply_qk_hadamard(q_work, k_work, random_sign=cfg.qk_hadamard_random_sign, seed=cfg.qk_hadamard_seed)
+
+
+def _quant_qk(t, cfg):
+    if cfg.qk_quant == "fp8_block":
+        c, sc = fp8_block_quant(t, block_s=cfg.fp8_block_size)
+        return c, sc, {"kind": "fp8_block", "block_s": cfg.fp8_block_size}
+    if cfg.qk_quant == "mxfp8":
+        c, sc = mxfp8_qk_quant(t, block_d=cfg.mxfp8_block_size)
+        return c, sc, {"kind": "mxfp8", "block_d": cfg.mxfp8_block_size}
+    raise ValueError(f"unsupported qk_quant: {cfg.qk_quant!r}")
+
+
+def _dequant_qk(fp8, scale, meta, dtype):
+    if meta["kind"] == "fp8_block":
+        return fp8_block_dequant(fp8, scale, block_s=meta["block_s"], dtype=dtype)
+    if meta["kind"] == "mxfp8":
+        return mxfp8_qk_dequant(fp8, scale, block_d=meta["block_d"], dtype=dtype)
+    raise ValueError(f"bad meta: {meta!r}")
+
+
+def _quant_v(t, cfg):
+    if cfg.v_quant == "fp8_channel":
+        c, sc = fp8_per_channel_quant(t)
+        return c, sc, {"kind": "fp8_channel"}
+    if cfg.v_quant == "fp8_block":
+        c, sc = fp8_block_quant(t, block_s=cfg.v_fp8_block_size)
+        return c, sc, {"kind": "fp8_block", "block_s": cfg.v_fp8_block_size}
+    if cfg.v_quant == "mxfp8":
+        c, sc = mxfp8_v_quant(t, block_s=cfg.v_mxfp8_block_size)
+        return c, sc, {"kind": "mxfp8", "block_s": cfg.v_mxfp8_block_size}
+    raise ValueError(f"unsupported v_quant: {cfg.v_quant!r}")
+
+
+def _dequant_v(fp8, scale, meta, dtype):
+    if meta["kind"] == "fp8_channel":
+        return fp8_per_channel_dequant(fp8, scale, dtype=dtype)
+    if meta["kind"] == "fp8_block":
+        return fp8_block_dequant(fp8, scale, block_s=meta["block_s"], dtype=dtype)
+    if meta["kind"] == "mxfp8":
+        return mxfp8_v_dequant(fp8, scale, block_s=meta["block_s"], dtype=dtype)
+    raise ValueError(f"bad meta: {meta!r}")
 
 
 @dataclass
