@@ -223,3 +223,28 @@ def test_full_length_wan_shapes_sampled_rows(gpu, config):
     print(f"config {config}: {st}")
     assert st["excess"] <= 1.0, f"config {config}: {st}"
     assert st["frac_equal"] >= 0.97, f"config {config}: {st}"
+
+
+@pytest.mark.parametrize("n", [1, 3, 17, 65, 129])
+@pytest.mark.parametrize("qm", [False, True])
+def test_tiny_and_odd_sequence_lengths(gpu, n, qm):
+    """S below one 64-key tile, one key past a tile, one row past the
+    128-query workgroup (waves of padding rows only); with Q smoothing, groups
+    of one row (n = 1) or of the whole sequence.  MX Q/K and channel V accept
+    any S."""
+    from low_bit_fake_quant import fake_quant_attention
+    from low_bit_fake_quant.attention import launch_sdpa
+    kw = dict(qk_quant="mxfp8", v_quant="fp8_channel", smoothing="full" if qm else "k_only", q_kmeans_k=None,
+              v_smooth_mode="off")
+    if qm:
+        kw["q_smooth_block_size"] = 1 if n == 1 else n
+    cfg = _cfg(**kw)
+    q, k, v = _inputs(n=n, d=64, seed=50 + n)
+    out = fake_quant_attention(q.to(gpu), k.to(gpu), v.to(gpu), cfg).cpu()
+    assert out.shape == q.shape and torch.isfinite(out.float()).all()
+    ref = opipe.fake_quant_attention(q, k, v, cfg)
+    c, m = cosine(out, ref), max_abs(out, ref)
+    assert c >= parity.COS_MIN and m <= parity.MAXABS, f"S={n}: cos={c:.7f} maxabs={m:.3e}"
+    sops, sm, _ = _operands(q, k, v, cfg, gpu)
+    st = parity.sdpa_replay(sops, launch_sdpa(sops, sm, q.dtype), sm)
+    assert st["excess"] <= 1.0, f"S={n}: {st}"
