@@ -41,6 +41,9 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
@@ -219,6 +222,23 @@ __device__ __forceinline__ void to_log2(const v16f (&s)[2], int key0, int g, int
   }
 }
 
+// Two fp32 values rounded (RNE) to the SDPA dtype and packed into one word,
+// low half the first: one packed conversion.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const f32x2 v = {a, b};
+  if constexpr (DT == kBF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+// The two halves of a packed word as fp32 (exact).
+template <int DT>
+__device__ __forceinline__ float lo_of(uint32_t w) { return from_bits<DT>(w & 0xffffu); }
+template <int DT>
+__device__ __forceinline__ float hi_of(uint32_t w) {
+  if constexpr (DT == kBF16) return __uint_as_float(w & 0xffff0000u);
+  else return from_bits<DT>(w >> 16);
+}
+
 // The lane's 32 P values (score layout) as packed SDPA-dtype pairs:
 // w[kb][j][k] holds registers 16 kb + 8 j + 2 k and + 1.
 template <int DT>
@@ -230,7 +250,24 @@ __device__ __forceinline__ void pack(const float (&p)[32], uint32_t (&w)[2][2][4
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int r = 16 * kb + 8 * j + 2 * k;
-        w[kb][j][k] = to_bits<DT>(p[r]) | (to_bits<DT>(p[r + 1]) << 16);
+        w[kb][j][k] = pack2<DT>(p[r], p[r + 1]);
+      }
+}
+
+// P as its SDPA-dtype rounding (whi) plus the rounding's exact residual,
+// rounded once more (wlo): p = hi + lo to ~16 significant bits.
+template <int DT>
+__device__ __forceinline__ void pack_split(const float (&p)[32], uint32_t (&whi)[2][2][4], uint32_t (&wlo)[2][2][4]) {
+  pack<DT>(p, whi);
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = 16 * kb + 8 * j + 2 * k;
+        const uint32_t h = whi[kb][j][k];
+        wlo[kb][j][k] = pack2<DT>(p[r] - lo_of<DT>(h), p[r + 1] - hi_of<DT>(h));  // exact differences
       }
 }
 
@@ -373,11 +410,7 @@ __global__ void __launch_bounds__(256, 2) sdpa_fwd_kernel(const SdpaArgs a) {
           for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
       }
       uint32_t whi[2][2][4], wlo[2][2][4];
-      pack<DT>(u, whi);
-      float res[32];
-#pragma unroll
-      for (int j = 0; j < 32; ++j) res[j] = u[j] - round_dt<DT>(u[j]);  // exact in fp32
-      pack<DT>(res, wlo);
+      pack_split<DT>(u, whi, wlo);
       pv<D, DT>(buf, li, g, whi, acc);
       pv<D, DT>(buf, li, g, wlo, acc);
       stage_store<D, true>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
