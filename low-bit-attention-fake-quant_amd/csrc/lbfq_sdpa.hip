@@ -19,16 +19,17 @@
 //     normalised P to the SDPA dtype -- the value the reference rounds --
 //     before the PV product.  The correction comes in log2 units from lbfq_qmk.
 //
-// Work decomposition: one wave = 32 queries of one (b, h), four independent
-// waves per workgroup, 64-key tiles.  Scores are computed transposed,
-// S^T = K Q^T: lane (i, g) = (lane % 32, lane / 32) holds query i and, in the
-// MFMA accumulator layout, keys 8 (r / 4) + 4 g + r % 4 (r = 0..15) of each
-// 32-key block.  The PV product O^T = V^T P^T consumes P in that layout: its
-// k-step j of a block contracts the keys of registers r = 8 j .. 8 j + 7, i.e.
-// 16 j + 4 g + {0..3} and 16 j + 8 + 4 g + {0..3} for lane group g, so each
-// lane reads its V^T operand as two 4-element pieces of one V^T row.
-// Operands come straight from global memory; the four waves of a workgroup
-// walk the same keys of one head, so the caches serve most of the re-reads.
+// Work decomposition: one wave = 32 queries of one (b, h), four waves per
+// workgroup, 64-key tiles.  The workgroup's 256 threads load each K and V^T
+// tile from global memory one tile ahead and stage it in a double-buffered
+// LDS area that all four waves read (one barrier per tile).  Scores are
+// computed transposed, S^T = K Q^T: lane (i, g) = (lane % 32, lane / 32)
+// holds query i and, in the MFMA accumulator layout, keys 8 (r / 4) + 4 g +
+// r % 4 (r = 0..15) of each 32-key block.  The PV product O^T = V^T P^T
+// consumes P in that layout: its k-step j of a block contracts the keys of
+// registers r = 8 j .. 8 j + 7, i.e. 16 j + 4 g + {0..3} and 16 j + 8 + 4 g +
+// {0..3} for lane group g; the staged V^T rows hold those eight keys next to
+// each other, so a lane reads its V^T operand as one 16-byte piece.
 #include <cmath>
 
 #include "lbfq_common.h"
