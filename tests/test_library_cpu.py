@@ -153,3 +153,41 @@ def test_rowtile_rejects_hadamard_with_v_modes():
         p.scale = 0x3000; p.amax_table = 0x4000; p.mx_block = 32
         assert lib.lbfq_rowtile(ctypes.byref(p), None) != 0
         assert b"Hadamard" in lib.lbfq_last_error()
+
+
+def test_sdpa_entry_points_reject_bad_arguments_without_a_gpu():
+    """lbfq_sdpa_dequant / lbfq_sdpa_fwd validate their parameters before any
+    HIP call: bad parameters return -1 with a message, with no device present.
+    (No pointer is dereferenced on these paths; fake addresses are enough.)"""
+    from low_bit_fake_quant import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = _lib.load(require_gpu=False)
+
+    def err(rc):
+        assert rc == -1
+        return lib.lbfq_last_error().decode()
+
+    assert "null params" in err(lib.lbfq_sdpa_fwd(None, None))
+    assert "null params" in err(lib.lbfq_sdpa_dequant(None, None))
+    fake = 0x1000
+    p = _lib.SdpaParams(B=1, H=2, S=256, D=128, s_pitch=256, q=fake, k=fake, v_t=fake, sdpa_dtype=2,
+                        sm_scale=0.125, out=fake, out_dtype=2)
+    for field, value, msg in (("D", 96, "D must be 64 or 128"), ("s_pitch", 200, "multiple of 128"),
+                              ("s_pitch", 128, "multiple of 128"), ("sdpa_dtype", 0, "bf16 or fp16"),
+                              ("out_dtype", 7, "bad output dtype 7"), ("v_t", None, "missing tensor"),
+                              ("qk_bias", fake, "bad qm groups")):
+        saved = getattr(p, field)
+        setattr(p, field, value)
+        assert msg in err(lib.lbfq_sdpa_fwd(ctypes.byref(p), None)), field
+        setattr(p, field, saved)
+    d = _lib.SdpaDequantParams(B=1, H=2, S=256, D=64, s_pitch=256, q_codes=fake, k_codes=fake, v_codes_t=fake,
+                               qk_mx=0, q_scale=fake, k_scale=fake, qk_block=64, v_kind=0, v_scale=fake,
+                               sdpa_dtype=2, q_out=fake, k_out=fake, v_t_out=fake)
+    for field, value, msg in (("D", 32, "D must be 64 or 128"), ("q_out", None, "missing output"),
+                              ("sdpa_dtype", 0, "bf16 or fp16"), ("v_kind", 3, "bad v_kind 3"),
+                              ("v_alpha", fake, "bad V smoothing block 0")):
+        saved = getattr(d, field)
+        setattr(d, field, value)
+        assert msg in err(lib.lbfq_sdpa_dequant(ctypes.byref(d), None)), field
+        setattr(d, field, saved)
