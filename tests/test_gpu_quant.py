@@ -91,3 +91,43 @@ def test_zero_block_and_error_messages(gpu):
         fp8_block_quant(torch.zeros(1, 100, 1, 64, device=gpu), block_s=64)
     with pytest.raises(ValueError, match=r"shape\[-1\] must be 64 or 128"):
         mxfp8_qk_quant(torch.zeros(1, 64, 1, 32, device=gpu))
+
+
+def test_non_finite_inputs_quantise_like_the_reference(gpu):
+    """The reference clamps with tl.minimum(tl.maximum(x / sc, -448), 448) and
+    takes amax with tl.max (quant_triton.py:47-49, 151-159, 240-244, 339-343),
+    Triton's maximum / minimum without NaN propagation, which return the
+    non-NaN operand (IEEE maxNum / minNum).  So a NaN element drops out of its
+    block's amax and quantises to -448 (code 0xFE); every other code and every
+    scale are those of the same input with the NaN read as 0.  (The CPU oracle
+    uses torch's NaN-propagating clamp and amax, so it is not the reference
+    here.)  +-inf: an fp8_block / channel scale becomes inf, inf / inf = NaN
+    gives -448; the MX scales clamp their E8M0 exponent, so +-inf gives +-448."""
+    from low_bit_fake_quant import fp8_block_quant, fp8_per_channel_quant, mxfp8_qk_quant, mxfp8_v_quant
+    quants = {
+        "fp8_block": (lambda t: fp8_block_quant(t, block_s=64), lambda t: oq.fp8_block_quant(t, 64)),
+        "channel": (fp8_per_channel_quant, oq.fp8_per_channel_quant),
+        "mx_qk": (lambda t: mxfp8_qk_quant(t, block_d=32), lambda t: oq.mxfp8_qk_quant(t, 32)),
+        "mx_v": (lambda t: mxfp8_v_quant(t, block_s=64), lambda t: oq.mxfp8_v_quant(t, 64)),
+    }
+    x = _inputs((1, 128, 2, 64), torch.bfloat16, seed=77)
+    pos = (0, 5, 1, 3)
+    for name, (gq, cq) in quants.items():
+        xn = x.clone()
+        xn[pos] = float("nan")
+        codes, sc = gq(xn.to(gpu))
+        c = codes.view(torch.uint8).cpu()
+        assert c[pos].item() == 0xFE, name
+        x0 = x.clone()
+        x0[pos] = 0.0
+        rc, rs = cq(x0)
+        rc = rc.clone()
+        rc[pos] = 0xFE
+        assert torch.equal(c, rc), name
+        assert torch.equal(sc.cpu(), rs), name
+        for val, code in ((float("inf"), 0x7E if name.startswith("mx") else 0xFE), (float("-inf"), 0xFE)):
+            xi = x.clone()
+            xi[pos] = val
+            codes, sc = gq(xi.to(gpu))
+            assert codes.view(torch.uint8).cpu()[pos].item() == code, (name, val)
+            assert bool(torch.isfinite(sc.float().cpu()).all()) == name.startswith("mx"), (name, val)
