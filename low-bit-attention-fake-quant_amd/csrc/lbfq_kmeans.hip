@@ -10,6 +10,9 @@
 //   update : fp64 sums per 1024-token chunk in token order, chunks added in
 //            order, c = (float)(sum / count), empty clusters keep c;
 //   labels : those of the last assign of `iters` rounds.
+// A slice whose assignment leaves every label as it was has converged: its
+// later rounds would recompute the same centroids and labels exactly, so its
+// workgroups skip them (a per-slice flag on the device, no host round trip).
 // The order is a stable counting sort of the labels (argsort stable=True).
 #include <mutex>
 #include "lbfq_common.h"
@@ -72,13 +75,19 @@ __device__ __forceinline__ void load_row(const void* x, int64_t idx, float (&v)[
 // One thread per token: its row in registers (16-byte loads), the slice's
 // centroids in LDS read as float4 broadcasts; each distance is the sequential
 // fmaf chain over d of the specification.
+// prev_changed: the flags of the previous round (NULL in the first round);
+// changed: this round's flags, set to 1 for a slice in which some label
+// changed.  They are zero on entry from the second round on; in the first
+// round every label counts as changed, so every slice's flag is written.
 template <int D, int DT>
 __global__ void __launch_bounds__(256) km_assign_kernel(const void* x, int64_t S, int64_t H, int K, const float* cent,
-                                                        int32_t* labels) {
+                                                        int32_t* labels, const int32_t* prev_changed,
+                                                        int32_t* changed) {
   __shared__ float4 c_lds[kMaxKAssign * D / 4];
   __shared__ float cn_lds[kMaxKAssign];
   const int64_t nblk_s = (S + 255) / 256;
   const int64_t bh = blockIdx.x / nblk_s;
+  if (prev_changed && prev_changed[bh] == 0) return;  // converged slice (uniform per workgroup)
   const int64_t t = (blockIdx.x % nblk_s) * 256 + threadIdx.x;
   const int64_t b = bh / H, h = bh % H;
   const float4* cg = reinterpret_cast<const float4*>(cent + bh * K * D);
@@ -135,7 +144,9 @@ __global__ void __launch_bounds__(256) km_assign_kernel(const void* x, int64_t S
     const float sc = fmaf(-2.0f, dot, cn_lds[j]);
     if (sc < best) { best = sc; bj = j; }
   }
+  const int32_t old = prev_changed ? labels[bh * S + t] : -1;
   labels[bh * S + t] = bj;
+  if (__any(old != bj) && (threadIdx.x & 63) == 0) changed[bh] = 1;
 }
 
 // fp64 per-cluster column sums of one kChunk-token chunk.  The chunk's tokens
@@ -149,7 +160,7 @@ constexpr int kUpdThreads = 512;
 template <int D, int DT>
 __global__ void __launch_bounds__(kUpdThreads) km_update_partial_kernel(const void* x, int64_t S, int64_t H, int K,
                                                                         const int32_t* labels, double* partial,
-                                                                        int32_t* counts) {
+                                                                        int32_t* counts, const int32_t* changed) {
   constexpr int NG = kUpdThreads / D;  // cluster groups
   constexpr int NW = kUpdThreads / 64;
   __shared__ int lab_s[kChunk];
@@ -159,6 +170,7 @@ __global__ void __launch_bounds__(kUpdThreads) km_update_partial_kernel(const vo
   __shared__ int wcnt[NW][kMaxKAssign];
   const int64_t nchunk = (S + kChunk - 1) / kChunk;
   const int64_t bh = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
+  if (changed[bh] == 0) return;  // converged slice (uniform per workgroup)
   const int64_t b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = c * kChunk;
@@ -226,12 +238,15 @@ __global__ void __launch_bounds__(kUpdThreads) km_update_partial_kernel(const vo
   }
 }
 
+// changed: this round's flags; clear_next: the next round's, cleared here
+// (the previous round's assignment, their last reader, has finished).
 __global__ void km_finalize_kernel(const double* partial, const int32_t* counts, int64_t nchunk, int K, int64_t D,
-                                   float* cent) {
+                                   float* cent, const int32_t* changed, int32_t* clear_next) {
   const int64_t bh = blockIdx.x / K;
   const int j = blockIdx.x % K;
   const int d = threadIdx.x;
-  if (d >= D) return;
+  if (j == 0 && d == 0) clear_next[bh] = 0;
+  if (d >= D || changed[bh] == 0) return;
   double tot = 0.0;
   int64_t cnt = 0;
   for (int64_t c = 0; c < nchunk; ++c) {
@@ -297,6 +312,7 @@ struct KmWs {
   float* cent;
   double* partial;
   int32_t* counts;
+  int32_t* changed;  // [2][BH]: the convergence flags of two consecutive rounds
 };
 
 KmWs carve(void* ws, int64_t BH, int64_t S, int64_t D, int K) {
@@ -308,6 +324,8 @@ KmWs carve(void* ws, int64_t BH, int64_t S, int64_t D, int K) {
   w.cent = reinterpret_cast<float*>(p);
   p += sizeof(float) * BH * K * D;
   w.counts = reinterpret_cast<int32_t*>(p);
+  p += sizeof(int32_t) * BH * nchunk * K;
+  w.changed = reinterpret_cast<int32_t*>(p);
   return w;
 }
 
@@ -316,7 +334,8 @@ KmWs carve(void* ws, int64_t BH, int64_t S, int64_t D, int K) {
 extern "C" int64_t lbfq_kmeans_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t D, int K) {
   const int64_t nchunk = (S + kChunk - 1) / kChunk;
   const int64_t BH = B * H;
-  return sizeof(double) * BH * nchunk * K * D + sizeof(float) * BH * K * D + sizeof(int32_t) * BH * nchunk * K;
+  return sizeof(double) * BH * nchunk * K * D + sizeof(float) * BH * K * D + sizeof(int32_t) * BH * nchunk * K +
+         sizeof(int32_t) * 2 * BH;
 }
 
 extern "C" int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int K, int iters,
@@ -339,12 +358,15 @@ extern "C" int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64
   const int rounds = iters > 0 ? iters : 1;
   for (int it = 0; it < rounds; ++it) {
     const dim3 ga(static_cast<unsigned>(BH * nblk_s)), gu(static_cast<unsigned>(BH * nchunk));
+    // round it writes flag slot it % 2, read by its update and finalize and by
+    // round it + 1's assignment; finalize clears slot (it + 1) % 2 first
+    int32_t* cur = w.changed + (it & 1) * BH;
+    const int32_t* prev = it == 0 ? nullptr : w.changed + ((it - 1) & 1) * BH;
 #define LBFQ_KM(DD, DT)                                                                                     \
-  hipLaunchKernelGGL((km_assign_kernel<DD, DT>), ga, dim3(256), 0, st, x, S, H, K, w.cent, labels);          \
+  hipLaunchKernelGGL((km_assign_kernel<DD, DT>), ga, dim3(256), 0, st, x, S, H, K, w.cent, labels, prev, cur); \
   if (it + 1 < rounds)                                                                                      \
     hipLaunchKernelGGL((km_update_partial_kernel<DD, DT>), gu, dim3(kUpdThreads), 0, st, x, S, H, K, labels,  \
-                       w.partial,                                                                           \
-                       w.counts);
+                       w.partial, w.counts, cur);
     if (D == 128) {
       if (dtype == kBF16) { LBFQ_KM(128, kBF16) } else if (dtype == kF16) { LBFQ_KM(128, kF16) } else { LBFQ_KM(128, kF32) }
     } else {
@@ -354,7 +376,7 @@ extern "C" int lbfq_kmeans(const void* x, int dtype, int64_t B, int64_t S, int64
     LBFQ_LAUNCH_CHECK("km_assign / km_update_partial");
     if (it + 1 == rounds) break;  // the last update does not change the labels
     hipLaunchKernelGGL(km_finalize_kernel, dim3(static_cast<unsigned>(BH * K)), dim3(static_cast<unsigned>(D)), 0, st,
-                       w.partial, w.counts, nchunk, K, D, w.cent);
+                       w.partial, w.counts, nchunk, K, D, w.cent, cur, w.changed + ((it + 1) & 1) * BH);
     LBFQ_LAUNCH_CHECK("km_finalize");
   }
   hipLaunchKernelGGL(km_sort_kernel, dim3(static_cast<unsigned>(BH)), dim3(kSortThreads), 0, st, labels, S, K, order,

@@ -148,3 +148,30 @@ def test_qmk_fused_k_quant_matches_separate_passes(gpu, d, blk, gathered):
     oc, osc = oq.fp8_block_quant(ks, block_s=blk)
     assert torch.equal(codes_b.cpu()[:, :, :s], oc.permute(0, 2, 1, 3))
     assert torch.equal(scale_b.cpu(), osc.permute(0, 2, 1))
+
+
+@pytest.mark.parametrize("iters", [10, 14])
+def test_kmeans_converged_slices_skip_later_rounds_bit_exact(gpu, iters):
+    """A slice whose assignment leaves every label unchanged has converged and
+    skips its later rounds; the result equals the oracle, which runs every
+    round.  Head 0 holds 32 well-separated clusters, one per initial stride
+    block (converged after two rounds: the skip path), head 1 pure noise
+    (labels still changing in the last round: no skip), in the same call."""
+    from low_bit_fake_quant import kmeans_reorder_tokens
+    g = torch.Generator().manual_seed(11)
+    cent = torch.randn(32, 128, generator=g) * 8
+    x0 = cent[torch.arange(2048) // 64] + 0.05 * torch.randn(2048, 128, generator=g)
+    x1 = torch.randn(2048, 128, generator=g)
+    x = torch.stack([x0, x1], 1).unsqueeze(0).to(torch.bfloat16)   # (1, S, H=2, D)
+
+    def labels_after(r):
+        return okm.kmeans_reorder_tokens(x, n_clusters=32, max_iters=r, seed=7)["labels"]
+    conv = [next((r for r in range(1, iters) if torch.equal(labels_after(r)[hh], labels_after(r + 1)[hh])), None)
+            for hh in (0, 1)]
+    assert conv[0] is not None and conv[0] < iters - 1, f"head 0 should converge early: {conv}"
+    assert conv[1] is None, f"head 1 should still change in the last round: {conv}"
+    r = kmeans_reorder_tokens(x.to(gpu), n_clusters=32, max_iters=iters, seed=7)
+    ref = okm.kmeans_reorder_tokens(x, n_clusters=32, max_iters=iters, seed=7)
+    assert torch.equal(r.labels.cpu(), ref["labels"])
+    assert torch.equal(r.order.cpu(), ref["order"])
+    assert torch.equal(r.tensor_reordered.cpu(), ref["tensor_reordered"])
