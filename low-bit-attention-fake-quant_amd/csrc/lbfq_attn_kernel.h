@@ -68,6 +68,9 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLog2Fp8Max = 8.807354922057604f;     // log2(448)
 constexpr float kLog2DynFloor = -39.86313713864835f;  // log2(1e-12)
+// Waves per workgroup: 4 (128 queries), or 8 (256 queries, one workgroup per
+// CU) for the kernels launch_p picks them for; the 4-wave figures below are
+// what the host requires of every call (s_pitch a multiple of kQB).
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kQB = kWaves * 32;  // queries per workgroup
@@ -108,8 +111,9 @@ struct KArgs {
 
 // Per-tile metadata staged in LDS next to the K / V^T codes.  The K side is
 // consumed by the softmax of the tile, the V side by its PV product.
+template <int NW>
 struct KMeta {
-  float bias[kWaves][kTN];  // qm correction (log2 units) of each wave's group
+  float bias[NW][kTN];      // qm correction (log2 units) of each wave's group
   uint32_t ke[kTN];         // MX: E8M0 bytes of the keys' D/32 chunks
   float ksc[kTN];           // fp8_block: scale of the 16-key group of each key
 };
@@ -691,8 +695,10 @@ __device__ __forceinline__ void valpha_outer(v16f (&acc)[NDB], const float* valp
   }
 }
 
-template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA, int BN>
-__global__ void __launch_bounds__(kThreads, attn_waves_per_simd(D, P_MODE, RB, BL, VALPHA, BN)) attn_fwd_kernel(const KArgs a) {
+template <int D, bool QK_MX, int P_MODE, int RB, int BL, bool VALPHA, int BN, int NW>
+__global__ void __launch_bounds__(NW * 64, attn_waves_per_simd(D, P_MODE, RB, BL, VALPHA, BN)) attn_fwd_kernel(const KArgs a) {
+  constexpr int kWaves = NW, kThreads = NW * 64, kQB = NW * 32;  // this kernel's workgroup
+  using KMeta = lbfq_attn::KMeta<NW>;
   static_assert(BN == 64 || BN == 128, "block_n is 64 or 128");
   constexpr bool BLASST = BL != 0;
   // BLASST with one fill value per row and tile, without V smoothing: a tile
@@ -707,7 +713,7 @@ __global__ void __launch_bounds__(kThreads, attn_waves_per_simd(D, P_MODE, RB, B
   constexpr bool HAS_EST = RB == RB_EST_BIAS;
 
   // rings: K tile i lives in slot i % 4, V^T tile i in slot i % 4 (76 KB at
-  // D = 128, so two workgroups share a CU).  The main loop runs four tile steps
+  // D = 128 with four waves, so two workgroups share a CU; 82 KB with eight).  The main loop runs four tile steps
   // per iteration, so every slot index is a compile-time constant there and
   // the LDS addresses are immediate offsets.
   // One ordered block: the small per-tile tables first, so that every access
@@ -1729,10 +1735,34 @@ int launch_b128_p2(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valph
 
 template <int P_MODE, int BN>
 int launch_p(const KArgs& a, int D, bool qk_mx, int rb, int bl, bool valpha, hipStream_t st) {
+  // Eight-wave workgroups (256 queries sharing each staged K / V^T tile) for
+  // the dense D = 128 kernels with fp8_block Q/K, no V smoothing and
+  // elementwise or dynamic P, where they measured faster than four; they
+  // need s_pitch to be a multiple of 256, so that ceil(S / 256) workgroups
+  // read no Q row past the pitch.  BLASST keeps four waves (its per-wave
+  // statistics are laid out for 128-query workgroups).
+  if constexpr (BN == 64 && P_MODE != 1) {
+    if (D == 128 && !qk_mx && bl == 0 && !valpha && a.P % 256 == 0) {
+      KArgs a8 = a;
+      a8.nqb = (a.S + 255) / 256;
+      dim3 grid8(static_cast<unsigned>(a.B * a.H * a8.nqb)), block8(8 * 64);
+#define LBFQ_L8(RBV) hipLaunchKernelGGL((attn_fwd_kernel<128, false, P_MODE, RBV, 0, false, BN, 8>), grid8, block8, 0, st, a8)
+      if (rb == RB_ONLINE) LBFQ_L8(RB_ONLINE);
+      else if (rb == RB_ONLINE_BIAS) LBFQ_L8(RB_ONLINE_BIAS);
+      else LBFQ_L8(RB_EST_BIAS);
+#undef LBFQ_L8
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) {
+        lbfq_set_error("lbfq_attention_fwd: launch failed: %s", hipGetErrorString(e));
+        return -2;
+      }
+      return 0;
+    }
+  }
   const int nblk = a.B * a.H * a.nqb;
   dim3 grid(static_cast<unsigned>(nblk)), block(kThreads);
 #define LBFQ_L(DD, MX, RBV, BL, VA) \
-  hipLaunchKernelGGL((attn_fwd_kernel<DD, MX, P_MODE, RBV, BL, VA, BN>), grid, block, 0, st, a)
+  hipLaunchKernelGGL((attn_fwd_kernel<DD, MX, P_MODE, RBV, BL, VA, BN, kWaves>), grid, block, 0, st, a)
 #define LBFQ_VA(DD, MX, RBV, BL) \
   if (valpha) LBFQ_L(DD, MX, RBV, BL, true); else LBFQ_L(DD, MX, RBV, BL, false)
 #define LBFQ_BL(DD, MX, RBV)                                                                     \
