@@ -281,7 +281,9 @@ def quantize_operands(prep: _Prep, cfg: QuantConfig, sm_scale: float) -> Quantiz
     b, s, h, d = prep.q.shape
     has_qm = prep.qm is not None
     validate_kernel_config(cfg, s=s, d=d, has_qm=has_qm, has_v_alpha=prep.v_alpha is not None)
-    P = round_up(s, 128)
+    # the pitch: a multiple of 256 (at most 255 zero rows), which the attention
+    # kernel's eight-wave (256-query) workgroups require
+    P = round_up(s, 256)
     signs = None
     if cfg.qk_hadamard and cfg.qk_hadamard_random_sign:
         signs = qk_signs_device(h, d, cfg.qk_hadamard_seed, prep.q.x.device)
