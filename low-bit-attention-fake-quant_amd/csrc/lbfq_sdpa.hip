@@ -19,10 +19,12 @@
 //     normalised P to the SDPA dtype -- the value the reference rounds --
 //     before the PV product.  The correction comes in log2 units from lbfq_qmk.
 //
-// Work decomposition: one wave = 32 queries of one (b, h), four waves per
-// workgroup, 64-key tiles.  The workgroup's 256 threads load each K and V^T
-// tile from global memory one tile ahead and stage it in a double-buffered
-// LDS area that all four waves read (one barrier per tile).  Scores are
+// Work decomposition: one wave = 32 queries of one (b, h), NW waves per
+// workgroup, 64-key tiles: NW = 8 (256 queries, one workgroup per CU, two
+// waves per SIMD) when that makes at least 256 workgroups, else 4 (128
+// queries, two workgroups per CU).  The workgroup's threads load each K and
+// V^T tile from global memory one tile ahead and stage it in a double-buffered
+// LDS area that all its waves read (one barrier per tile).  Scores are
 // computed transposed, S^T = K Q^T: lane (i, g) = (lane % 32, lane / 32)
 // holds query i and, in the MFMA accumulator layout, keys 8 (r / 4) + 4 g +
 // r % 4 (r = 0..15) of each 32-key block.  The PV product O^T = V^T P^T
@@ -112,7 +114,7 @@ struct SdpaArgs {
   const int32_t* out_row_map;
 };
 
-// LDS staging of one 64-key tile, shared by the workgroup's four waves and
+// LDS staging of one 64-key tile, shared by the workgroup's waves and
 // double-buffered: the K rows (D bf16 each, pitch KP bytes) and the V^T rows
 // (64 keys each, pitch VP bytes).  The pitches are 16 bytes past a multiple of
 // 128 so that the eight rows one ds_read_b128 phase touches fall on distinct
@@ -125,43 +127,50 @@ struct Stage {
   static constexpr int VP = 2 * 64 + 16;
   static constexpr int KBYTES = 64 * KP;
   static constexpr int BUF = KBYTES + D * VP;
-  static constexpr int KCH = 64 * D / 8 / 256;  // 16-byte K chunks per thread
-  static constexpr int VCH = D * 8 / 256;       // 16-byte V^T chunks per thread
+};
+// The copies of a tile per thread of an NW-wave workgroup.
+template <int D, int NW>
+struct Copy {
+  static constexpr int T = 64 * NW;           // threads per workgroup
+  static constexpr int KCH = 64 * D / 8 / T;  // 16-byte K chunks per thread
+  static constexpr int VCH = D * 8 / T;       // 16-byte V^T chunks per thread
 };
 
 // global -> registers: the thread's K and V^T chunks of the tile at key0
-template <int D, bool WITH_V>
+template <int D, int NW, bool WITH_V>
 __device__ __forceinline__ void stage_load(const uint16_t* kbase, const uint16_t* vbase, int P, int key0, int tid,
-                                           u32x4 (&kr)[Stage<D>::KCH], u32x4 (&vr)[Stage<D>::VCH]) {
+                                           u32x4 (&kr)[Copy<D, NW>::KCH], u32x4 (&vr)[Copy<D, NW>::VCH]) {
+  using C = Copy<D, NW>;
   constexpr int CPR = D / 8;  // K chunks per row
 #pragma unroll
-  for (int i = 0; i < Stage<D>::KCH; ++i) {
-    const int c = tid + 256 * i, row = c / CPR, col = c % CPR;
+  for (int i = 0; i < C::KCH; ++i) {
+    const int c = tid + C::T * i, row = c / CPR, col = c % CPR;
     kr[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<size_t>(key0 + row) * D + 8 * col);
   }
   if constexpr (WITH_V) {
 #pragma unroll
-    for (int i = 0; i < Stage<D>::VCH; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+    for (int i = 0; i < C::VCH; ++i) {
+      const int c = tid + C::T * i, row = c >> 3, kc = c & 7;
       vr[i] = *reinterpret_cast<const u32x4*>(vbase + static_cast<size_t>(row) * P + key0 + 8 * kc);
     }
   }
 }
 
 // registers -> LDS buffer (the key permutation of V^T applied here)
-template <int D, bool WITH_V>
-__device__ __forceinline__ void stage_store(uint8_t* buf, int tid, const u32x4 (&kr)[Stage<D>::KCH],
-                                            const u32x4 (&vr)[Stage<D>::VCH]) {
+template <int D, int NW, bool WITH_V>
+__device__ __forceinline__ void stage_store(uint8_t* buf, int tid, const u32x4 (&kr)[Copy<D, NW>::KCH],
+                                            const u32x4 (&vr)[Copy<D, NW>::VCH]) {
+  using C = Copy<D, NW>;
   constexpr int CPR = D / 8;
 #pragma unroll
-  for (int i = 0; i < Stage<D>::KCH; ++i) {
-    const int c = tid + 256 * i, row = c / CPR, col = c % CPR;
+  for (int i = 0; i < C::KCH; ++i) {
+    const int c = tid + C::T * i, row = c / CPR, col = c % CPR;
     *reinterpret_cast<u32x4*>(buf + row * Stage<D>::KP + 16 * col) = kr[i];
   }
   if constexpr (WITH_V) {
 #pragma unroll
-    for (int i = 0; i < Stage<D>::VCH; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+    for (int i = 0; i < C::VCH; ++i) {
+      const int c = tid + C::T * i, row = c >> 3, kc = c & 7;
       // keys 16 G + 8 h + [0,4) -> positions 16 G + 4 h + [0,4); + [4,8) -> 16 G + 8 + 4 h + [0,4)
       uint8_t* rp = buf + Stage<D>::KBYTES + row * Stage<D>::VP + 2 * (16 * (kc >> 1) + 4 * (kc & 1));
       *reinterpret_cast<u32x2*>(rp) = vr[i].xy;
@@ -291,24 +300,26 @@ __device__ __forceinline__ void pv(const uint8_t* buf, int li, int g, const uint
   }
 }
 
-template <int D, bool BIAS, int DT>
-__global__ void __launch_bounds__(256, 2) sdpa_fwd_kernel(const SdpaArgs a) {
+template <int D, bool BIAS, int DT, int NW>
+__global__ void __launch_bounds__(NW * 64, 2) sdpa_fwd_kernel(const SdpaArgs a) {
   constexpr int NKS = D / 16, NDB = D / 32;
   using St = Stage<D>;
   __shared__ __align__(16) uint8_t lds[2 * St::BUF];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, g = lane >> 5;
-  const int nqb = a.P / 128;
+  constexpr int QB = 32 * NW;  // queries per workgroup
+  const int nqb = (a.P + QB - 1) / QB;
   const int bh = blockIdx.x / nqb, qb = blockIdx.x - bh * nqb;
   const int S = a.S, P = a.P;
   // every wave takes part in the staging and the barriers; a wave whose rows
-  // are all padding (rows [S, P) of q are zero) computes and stores nothing
-  const int qi = qb * 128 + wave * 32 + li;
+  // are all padding (rows [S, P) of q are zero; rows past the pitch read the
+  // last one) computes and stores nothing
+  const int qi = qb * QB + wave * 32 + li;
 
   uint4 qop[NKS];
   {
-    const uint16_t* qrow = a.q + (static_cast<size_t>(bh) * P + qi) * D + 8 * g;
+    const uint16_t* qrow = a.q + (static_cast<size_t>(bh) * P + (qi < P ? qi : P - 1)) * D + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qop[ks] = *reinterpret_cast<const uint4*>(qrow + 16 * ks);
   }
@@ -321,7 +332,7 @@ __global__ void __launch_bounds__(256, 2) sdpa_fwd_kernel(const SdpaArgs a) {
   const uint16_t* kbase = a.k + static_cast<size_t>(bh) * P * D;
   const uint16_t* vbase = a.v_t + static_cast<size_t>(bh) * D * P;
   const int nt = (S + 63) / 64;
-  u32x4 kr[St::KCH], vr[St::VCH];
+  u32x4 kr[Copy<D, NW>::KCH], vr[Copy<D, NW>::VCH];
 
   v16f acc[NDB];
 #pragma unroll
@@ -333,14 +344,14 @@ __global__ void __launch_bounds__(256, 2) sdpa_fwd_kernel(const SdpaArgs a) {
   if constexpr (BIAS) {
     // pass 1: the row's max and sum (each lane over its own keys, merged at the end)
     float m = -INFINITY, l = 0.0f;
-    stage_load<D, false>(kbase, vbase, P, 0, tid, kr, vr);
-    stage_store<D, false>(lds, tid, kr, vr);
+    stage_load<D, NW, false>(kbase, vbase, P, 0, tid, kr, vr);
+    stage_store<D, NW, false>(lds, tid, kr, vr);
     __syncthreads();
     for (int t = 0; t < nt; ++t) {
       const uint8_t* buf = lds + (t & 1) * St::BUF;
       v16f s[2];
       scores<D, DT>(buf, li, g, qop, s);
-      stage_load<D, false>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
+      stage_load<D, NW, false>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
       float u[32];
       to_log2<true, DT>(s, 64 * t, g, S, a.sml2, brow, u);
       float tmax = u[0];
@@ -353,21 +364,21 @@ __global__ void __launch_bounds__(256, 2) sdpa_fwd_kernel(const SdpaArgs a) {
       for (int j = 0; j < 32; ++j) sum += __builtin_amdgcn_exp2f(u[j] - ms);
       l = l * __builtin_amdgcn_exp2f(m - ms) + sum;
       m = m_new;
-      stage_store<D, false>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
+      stage_store<D, NW, false>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
       __syncthreads();
     }
     const float mo = __shfl_xor(m, 32, 64), lo = __shfl_xor(l, 32, 64);
     const float mrow = fmaxf(m, mo);  // finite: key 0 is valid
     const float inv = 1.0f / (l * __builtin_amdgcn_exp2f(m - mrow) + lo * __builtin_amdgcn_exp2f(mo - mrow));
     // pass 2: P = dtype(exp2(u - max) / sum), O = P V
-    stage_load<D, true>(kbase, vbase, P, 0, tid, kr, vr);
-    stage_store<D, true>(lds, tid, kr, vr);
+    stage_load<D, NW, true>(kbase, vbase, P, 0, tid, kr, vr);
+    stage_store<D, NW, true>(lds, tid, kr, vr);
     __syncthreads();
     for (int t = 0; t < nt; ++t) {
       const uint8_t* buf = lds + (t & 1) * St::BUF;
       v16f s[2];
       scores<D, DT>(buf, li, g, qop, s);
-      stage_load<D, true>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
+      stage_load<D, NW, true>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
       float u[32];
       to_log2<true, DT>(s, 64 * t, g, S, a.sml2, brow, u);
 #pragma unroll
@@ -375,20 +386,20 @@ __global__ void __launch_bounds__(256, 2) sdpa_fwd_kernel(const SdpaArgs a) {
       uint32_t w[2][2][4];
       pack<DT>(u, w);
       pv<D, DT>(buf, li, g, w, acc);
-      stage_store<D, true>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
+      stage_store<D, NW, true>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
       __syncthreads();
     }
   } else {
     // online softmax; P as its SDPA-dtype rounding plus the rounded residual
     float m = -INFINITY, l = 0.0f;
-    stage_load<D, true>(kbase, vbase, P, 0, tid, kr, vr);
-    stage_store<D, true>(lds, tid, kr, vr);
+    stage_load<D, NW, true>(kbase, vbase, P, 0, tid, kr, vr);
+    stage_store<D, NW, true>(lds, tid, kr, vr);
     __syncthreads();
     for (int t = 0; t < nt; ++t) {
       const uint8_t* buf = lds + (t & 1) * St::BUF;
       v16f s[2];
       scores<D, DT>(buf, li, g, qop, s);
-      stage_load<D, true>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
+      stage_load<D, NW, true>(kbase, vbase, P, 64 * (t + 1 < nt ? t + 1 : t), tid, kr, vr);
       float u[32];
       to_log2<false, DT>(s, 64 * t, g, S, a.sml2, nullptr, u);
       float tmax = u[0];
@@ -414,7 +425,7 @@ __global__ void __launch_bounds__(256, 2) sdpa_fwd_kernel(const SdpaArgs a) {
       pack_split<DT>(u, whi, wlo);
       pv<D, DT>(buf, li, g, whi, acc);
       pv<D, DT>(buf, li, g, wlo, acc);
-      stage_store<D, true>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
+      stage_store<D, NW, true>(lds + ((t + 1) & 1) * St::BUF, tid, kr, vr);  // idle after the last tile
       __syncthreads();
     }
     inv_l = 1.0f / xor32_add(l);
@@ -602,10 +613,18 @@ extern "C" int lbfq_sdpa_fwd(const lbfq_sdpa_params* p, lbfq_stream_t stream) {
   a.out = p->out;
   a.out_dtype = p->out_dtype;
   a.out_row_map = p->out_row_map;
-  const dim3 grid(static_cast<unsigned>(p->B * p->H * (p->s_pitch / 128))), block(256);
+  // eight-wave workgroups (256 queries, one per CU) where there are enough of
+  // them to fill the chip; four-wave ones (two per CU) for small problems
+  const int64_t nwg8 = p->B * p->H * ((p->s_pitch + 255) / 256);
+  const bool w8 = nwg8 >= 256;
+  const dim3 grid(static_cast<unsigned>(w8 ? nwg8 : p->B * p->H * (p->s_pitch / 128))), block(w8 ? 512 : 256);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bias = p->qk_bias != nullptr, bf = p->sdpa_dtype == kBF16;
-#define LBFQ_SD(DD, BI, DT) hipLaunchKernelGGL((sdpa_fwd_kernel<DD, BI, DT>), grid, block, 0, st, a)
+#define LBFQ_SD(DD, BI, DT)                                                             \
+  do {                                                                                  \
+    if (w8) hipLaunchKernelGGL((sdpa_fwd_kernel<DD, BI, DT, 8>), grid, block, 0, st, a); \
+    else hipLaunchKernelGGL((sdpa_fwd_kernel<DD, BI, DT, 4>), grid, block, 0, st, a);    \
+  } while (0)
 #define LBFQ_SD_DT(DD, BI) \
   if (bf) LBFQ_SD(DD, BI, kBF16); else LBFQ_SD(DD, BI, kF16)
 #define LBFQ_SD_BI(DD) \

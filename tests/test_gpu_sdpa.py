@@ -20,7 +20,7 @@ import pytest
 import torch
 
 import parity
-from conftest import cosine, max_abs
+from conftest import cosine, cpu_randn, max_abs
 from oracle import pipeline as opipe
 
 pytestmark = pytest.mark.gpu
@@ -223,6 +223,28 @@ def test_full_length_wan_shapes_sampled_rows(gpu, config):
     print(f"config {config}: {st}")
     assert st["excess"] <= 1.0, f"config {config}: {st}"
     assert st["frac_equal"] >= 0.97, f"config {config}: {st}"
+
+
+@pytest.mark.parametrize("qm", [False, True])
+def test_eight_wave_workgroups_past_the_pitch(gpu, qm):
+    """Eight-wave (256-query) workgroups, used when there are at least 256 of
+    them, with a pitch that is an odd multiple of 128 (S = 21888, 3 heads:
+    258 workgroups, the last one's upper half past the pitch): the float64
+    replay on 1024 sampled rows of each head, 128 of them the last rows."""
+    from low_bit_fake_quant.attention import launch_sdpa
+    s, h = 21888, 3
+    kw = dict(qk_quant="mxfp8", v_quant="fp8_channel", smoothing="full" if qm else "k_only", q_kmeans_k=None,
+              v_smooth_mode="off", q_smooth_block_size=128)
+    cfg = _cfg(**kw)
+    q, k, v = (cpu_randn(1, s, h, 128, seed=sd, scale=1.5) for sd in (31, 32, 33))
+    sops, sm, dt = _operands(q, k, v, cfg, gpu)
+    assert sops.P == s and (s // 128) % 2 == 1 and h * ((s + 255) // 256) >= 256
+    out = launch_sdpa(sops, sm, q.dtype)
+    g = torch.Generator().manual_seed(6)
+    rows = torch.cat([torch.randperm(s - 128, generator=g)[:896], torch.arange(s - 128, s)])
+    st = parity.sdpa_replay(sops, out, sm, rows=rows)
+    assert st["excess"] <= 1.0, st
+    assert st["frac_equal"] >= 0.97, st
 
 
 @pytest.mark.parametrize("n", [1, 3, 17, 65, 129])
