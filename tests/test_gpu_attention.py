@@ -516,3 +516,30 @@ def test_tiny_and_odd_sequence_lengths(gpu, n, blasst):
     out = fake_quant_attention(q.to(gpu), k.to(gpu), v.to(gpu), cfg).cpu()
     assert out.shape == q.shape and torch.isfinite(out).all()
     check_parity(out, q, k, v, cfg, f"S={n}{'/blasst' if blasst else ''}")
+
+
+EIGHT_WAVE_CASES = {
+    "elementwise_online_konly": dict(qk_quant="fp8_block", fp8_block_size=64, v_quant="fp8_channel",
+                                     smoothing="k_only", q_kmeans_k=None, p_quant="elementwise"),
+    "dynamic_online_full": dict(qk_quant="fp8_block", fp8_block_size=64, v_quant="fp8_channel", smoothing="full",
+                                q_smooth_block_size=64, q_kmeans_k=None, p_quant="dynamic"),
+    "dynamic_qmk_kmeans": dict(qk_quant="fp8_block", fp8_block_size=64, v_quant="fp8_channel", smoothing="full",
+                               q_smooth_block_size=64, q_kmeans_k=4, p_quant="dynamic", rowmax_mode="qm_k"),
+}
+
+
+@pytest.mark.parametrize("n", [64, 320, 960])
+@pytest.mark.parametrize("name", sorted(EIGHT_WAVE_CASES))
+def test_eight_wave_workgroups_ragged(gpu, name, n):
+    """Dense fp8_block Q/K at D = 128 without V smoothing runs 256-query
+    (eight-wave) workgroups.  S = 64, 320 and 960 leave the last workgroup
+    with 64, 64 and 192 valid queries of 256: six, six and two of its waves
+    hold no valid query but still stage their share of every K/V tile and
+    meet every barrier.  One case per row-max mode (online, online + Q-smoothing bias,
+    qm_k estimate) and P mode (elementwise, dynamic)."""
+    from low_bit_fake_quant import fake_quant_attention
+    cfg = _cfg(**EIGHT_WAVE_CASES[name])
+    q, k, v = _inputs(n=n, seed=50 + n, q_clusters=4 if n >= 256 else 0, v_bias=True)
+    out = fake_quant_attention(q.to(gpu), k.to(gpu), v.to(gpu), cfg).cpu()
+    assert out.shape == q.shape and torch.isfinite(out).all()
+    check_parity(out, q, k, v, cfg, f"8w-{name}-S={n}")
