@@ -573,7 +573,8 @@ def main() -> int:
         costs = issue_costs(dev)
         props = torch.cuda.get_device_properties(dev)
         simds = props.multi_processor_count * 4
-        # (wave of 32 queries, 64-key tile) pairs per SIMD: workgroups of 4 waves x 128 queries
+        # (wave of 32 queries, 64-key tile) pairs per SIMD: workgroups of 4 waves x 128 queries (eight-wave
+        # workgroups of 256 queries launch as many waves wherever ceil(S / 256) = ceil(S / 128) / 2, as at S = 32760)
         wave_tiles = b * h * ((s + 127) // 128) * 4 * ((s + 63) // 64) / simds
         info = clock_sample(ops, cfg, sm_scale, 120, attention_flops(n_real, h, d, b), launch_attention,
                             quiet=True)
