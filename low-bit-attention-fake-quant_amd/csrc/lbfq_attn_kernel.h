@@ -6,12 +6,12 @@
 // (v_mfma[_scale]_f32_32x32x64_f8f6f4) and applies the scales outside, or
 // through the E8M0 block scales of the MFMA for the MX formats.
 //
-// Work decomposition: one workgroup = 4 waves = 128 queries of one (b, h);
-// each wave owns 32 queries.  K and V^T tiles of 64 keys (== the reference
-// block_n) are copied global -> LDS directly (four-slot K and V^T rings,
-// staged three and two tiles ahead) together with the per-tile
-// metadata (qm correction row, K/V scales, V block means), and shared by the
-// 4 waves.  Scores are computed transposed, S^T = K Q^T, so every lane owns
+// Work decomposition: one workgroup = NW waves = 32 NW queries of one (b, h)
+// (NW = 4, or 8 for the dense fp8_block D = 128 kernels); each wave owns 32
+// queries.  K and V^T tiles of 64 keys (== the reference block_n) are copied
+// global -> LDS directly (four-slot K and V^T rings, staged three and two
+// tiles ahead) together with the per-tile metadata (qm correction row, K/V
+// scales, V block means), and shared by the workgroup's waves.  Scores are computed transposed, S^T = K Q^T, so every lane owns
 // exactly one query: lane l holds query l % 32 and, in lane group
 // g = l / 32, the 32 keys 32t + 16g + r (t in {0,1}, r in 0..15) of the tile.
 // K rows are permuted in LDS so that the MFMA accumulator layout yields that
