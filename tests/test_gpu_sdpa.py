@@ -225,18 +225,21 @@ def test_full_length_wan_shapes_sampled_rows(gpu, config):
     assert st["frac_equal"] >= 0.97, f"config {config}: {st}"
 
 
+@pytest.mark.parametrize("d,dtype", [(64, torch.bfloat16), (128, torch.bfloat16), (128, torch.float16)])
 @pytest.mark.parametrize("qm", [False, True])
-def test_eight_wave_workgroups_past_the_pitch(gpu, qm):
+def test_eight_wave_workgroups_past_the_pitch(gpu, qm, d, dtype):
     """Eight-wave (256-query) workgroups, used when there are at least 256 of
     them, with a pitch that is an odd multiple of 128 (S = 21888, 3 heads:
-    258 workgroups, the last one's upper half past the pitch): the float64
-    replay on 1024 sampled rows of each head, 128 of them the last rows."""
+    258 workgroups, the last one's upper half past the pitch), at both head
+    dims (one 16-byte K and one V^T chunk per thread per tile at D = 64, two
+    at D = 128), bf16 and fp16: the float64 replay on 1024 sampled rows of
+    each head, 128 of them the last rows."""
     from low_bit_fake_quant.attention import launch_sdpa
     s, h = 21888, 3
     kw = dict(qk_quant="mxfp8", v_quant="fp8_channel", smoothing="full" if qm else "k_only", q_kmeans_k=None,
               v_smooth_mode="off", q_smooth_block_size=128)
     cfg = _cfg(**kw)
-    q, k, v = (cpu_randn(1, s, h, 128, seed=sd, scale=1.5) for sd in (31, 32, 33))
+    q, k, v = (cpu_randn(1, s, h, d, seed=sd, scale=1.5, dtype=dtype) for sd in (31, 32, 33))
     sops, sm, dt = _operands(q, k, v, cfg, gpu)
     assert sops.P == s and (s // 128) % 2 == 1 and h * ((s + 255) // 256) >= 256
     out = launch_sdpa(sops, sm, q.dtype)
