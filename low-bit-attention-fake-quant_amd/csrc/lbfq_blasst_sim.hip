@@ -20,10 +20,14 @@
 //                     block keeps the first block of largest max-over-rows bmax
 //                     (blasst_skip.py:375-386, 584-619)
 //
-// Work decomposition: one thread per query row (its q row and its output row
-// in registers), one wave per 64 rows of one head; every lane reads the same
-// key row at a time (wave-uniform loads).  Tile statistics are combined across
-// the two waves of a 128-row tile by ordered-integer atomicMax.
+// Work decomposition: one wave per 64 / LPR query rows of one head, LPR =
+// D / 64 lanes per row, each holding 64 dimensions of the row's q and output
+// in registers; the lanes of a row read the same key rows at a time, four
+// keys' dot products as four independent chains.  The online and static-P
+// rungs form each key block's scores once, in the block-max pass, and keep
+// them in LDS (32 KB per wave at D = 64, 16 KB at D = 128) for the
+// accumulation pass.  Tile statistics are combined across the waves of a
+// 128-row tile by ordered-integer atomicMax.
 #include <algorithm>
 
 #include "lbfq_common.h"
@@ -33,7 +37,6 @@ using namespace lbfq;
 
 namespace {
 
-constexpr int kRows = 64;    // rows per workgroup (one wave)
 constexpr int kTileQ = 128;  // query tile / key block (QUERY_TILE, KEY_BLOCK)
 constexpr float kDenomFloor = 1e-30f;
 
@@ -103,42 +106,92 @@ __global__ void __launch_bounds__(256) head_quant_kernel(const void* x, int64_t 
   }
 }
 
-// ---- scores of one row against one key -------------------------------------------
+// ---- scores of one row against key rows ---------------------------------------
+// A row's D dimensions are split over LPR = D / 64 lanes (lane l holds
+// row l % (64 / LPR), dimensions [l / (64 / LPR) * 64, + 64)), so a lane keeps
+// 64 q and 64 output values and D = 128 runs more than one wave per SIMD.
+// Each lane's partial dot product is a chain in dimension order; the LPR
+// partials are then added (partner lanes l and l ^ 32 form the same sum).
 template <int D>
-__device__ __forceinline__ float dot_row(const float (&q)[D], const float* krow, float sm_scale) {
+struct Split {
+  static constexpr int LPR = D / 64;     // lanes per row
+  static constexpr int DL = D / LPR;     // dimensions per lane
+  static constexpr int RPW = 64 / LPR;   // rows per wave
+};
+
+template <int DL, int LPR>
+__device__ __forceinline__ float row_sum(float acc) {
+  // lanes l, l ^ (64 / LPR), ... hold the partials of one row; every one of
+  // them forms the same sum (pairwise, commutative at each step)
+#pragma unroll
+  for (int m = 64 / LPR; m < 64; m <<= 1) acc += __shfl_xor(acc, m, 64);
+  return acc;
+}
+
+template <int DL, int LPR>
+__device__ __forceinline__ float dot_part(const float (&q)[DL], const float* krow, float sm_scale) {
   float acc = 0.0f;
 #pragma unroll
-  for (int d = 0; d < D; d += 4) {
+  for (int d = 0; d < DL; d += 4) {
     const float4 k4 = *reinterpret_cast<const float4*>(krow + d);
     acc = fmaf(q[d], k4.x, acc);
     acc = fmaf(q[d + 1], k4.y, acc);
     acc = fmaf(q[d + 2], k4.z, acc);
     acc = fmaf(q[d + 3], k4.w, acc);
   }
-  return acc * sm_scale;
+  return row_sum<DL, LPR>(acc) * sm_scale;
+}
+
+// dot_part for four consecutive keys (rows `stride` floats apart): four
+// independent chains, each in the order of dot_part.
+template <int DL, int LPR>
+__device__ __forceinline__ void dot_part4(const float (&q)[DL], const float* krow, int64_t stride, float sm_scale,
+                                          float (&s)[4]) {
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int d = 0; d < DL; d += 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 k4 = *reinterpret_cast<const float4*>(krow + i * stride + d);
+      a[i] = fmaf(q[d], k4.x, a[i]);
+      a[i] = fmaf(q[d + 1], k4.y, a[i]);
+      a[i] = fmaf(q[d + 2], k4.z, a[i]);
+      a[i] = fmaf(q[d + 3], k4.w, a[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s[i] = row_sum<DL, LPR>(a[i]) * sm_scale;
+  }
 }
 
 // Pass 1: per row the final max; per (tile, key block) the max over the tile's
 // rows of bmax_j - rm_j and of bmax_j.
 template <int D>
-__global__ void __launch_bounds__(kRows) scan_kernel(const float* q, const float* k, int64_t S, int64_t H,
-                                                     float sm_scale, float* final_max, uint32_t* tile_margin,
-                                                     uint32_t* tile_bmax) {
+__global__ void __launch_bounds__(64) scan_kernel(const float* q, const float* k, int64_t S, int64_t H,
+                                                  float sm_scale, float* final_max, uint32_t* tile_margin,
+                                                  uint32_t* tile_bmax) {
+  using SP = Split<D>;
+  constexpr int DL = SP::DL;
   const int64_t h = blockIdx.y;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRows + threadIdx.x;
+  const int r = threadIdx.x % SP::RPW, part = threadIdx.x / SP::RPW;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * SP::RPW + r;
   const int64_t nb = S / kTileQ, mt = row / kTileQ;
-  float qr[D];
+  float qr[DL];
 #pragma unroll
-  for (int d = 0; d < D; d += 4) {
-    const float4 v = *reinterpret_cast<const float4*>(q + (row * H + h) * D + d);
+  for (int d = 0; d < DL; d += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(q + (row * H + h) * D + part * DL + d);
     qr[d] = v.x; qr[d + 1] = v.y; qr[d + 2] = v.z; qr[d + 3] = v.w;
   }
   float rm = -INFINITY;
   for (int64_t j = 0; j < nb; ++j) {
     float bmax = -INFINITY;
-    for (int kk = 0; kk < kTileQ; ++kk) {
+    for (int kk = 0; kk < kTileQ; kk += 4) {
       const int64_t key = j * kTileQ + kk;
-      bmax = fmaxf(bmax, dot_row<D>(qr, k + (key * H + h) * D, sm_scale));
+      float s4[4];
+      dot_part4<DL, SP::LPR>(qr, k + (key * H + h) * D + part * DL, H * D, sm_scale, s4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bmax = fmaxf(bmax, s4[i]);
     }
     rm = fmaxf(rm, bmax);
     const float tm = wave_max(bmax - rm), tb = wave_max(bmax);
@@ -148,7 +201,7 @@ __global__ void __launch_bounds__(kRows) scan_kernel(const float* q, const float
       atomicMax(tile_bmax + o, ordered_bits(tb));
     }
   }
-  final_max[h * S + row] = rm;
+  if (part == 0) final_max[h * S + row] = rm;
 }
 
 // Tile keep masks for T thresholds, with the empty-tile safeguard.
@@ -184,17 +237,24 @@ __global__ void __launch_bounds__(256) keep_kernel(const uint32_t* tile_margin, 
 
 // Pass 2: one rung (exact / online / static P with a tile keep mask).
 template <int D, int MODE>
-__global__ void __launch_bounds__(kRows) attend_kernel(const float* q, const float* k, const float* v, int64_t S,
-                                                       int64_t H, float sm_scale, int round_p, const float* final_max,
-                                                       const uint8_t* keep, float* out, float* dropped,
-                                                       unsigned long long* p_counts, double* p_sqerr) {
+__global__ void __launch_bounds__(64) attend_kernel(const float* q, const float* k, const float* v, int64_t S,
+                                                    int64_t H, float sm_scale, int round_p, const float* final_max,
+                                                    const uint8_t* keep, float* out, float* dropped,
+                                                    unsigned long long* p_counts, double* p_sqerr) {
+  using SP = Split<D>;
+  constexpr int DL = SP::DL, RPW = SP::RPW;
+  // the block's scores of the wave's rows (column r), formed in the block-max
+  // pass and read back by the lanes of the same row in the accumulation pass
+  __shared__ float sc[MODE != 0 ? kTileQ * RPW : 1];
   const int64_t h = blockIdx.y;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRows + threadIdx.x;
+  const int r = threadIdx.x % RPW, part = threadIdx.x / RPW;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPW + r;
   const int64_t nb = S / kTileQ, mt = row / kTileQ;
-  float qr[D], acc[D];
+  const int64_t dofs = part * DL;  // this lane's dimensions of q, v and the output row
+  float qr[DL], acc[DL];
 #pragma unroll
-  for (int d = 0; d < D; d += 4) {
-    const float4 x = *reinterpret_cast<const float4*>(q + (row * H + h) * D + d);
+  for (int d = 0; d < DL; d += 4) {
+    const float4 x = *reinterpret_cast<const float4*>(q + (row * H + h) * D + dofs + d);
     qr[d] = x.x; qr[d + 1] = x.y; qr[d + 2] = x.z; qr[d + 3] = x.w;
     acc[d] = acc[d + 1] = acc[d + 2] = acc[d + 3] = 0.0f;
   }
@@ -208,9 +268,15 @@ __global__ void __launch_bounds__(kRows) attend_kernel(const float* q, const flo
     float rescale = 1.0f;
     if (MODE != 0) {
       float bmax = -INFINITY;
-      for (int kk = 0; kk < kTileQ; ++kk) {
+      for (int kk = 0; kk < kTileQ; kk += 4) {
         const int64_t key = j * kTileQ + kk;
-        bmax = fmaxf(bmax, dot_row<D>(qr, k + (key * H + h) * D, sm_scale));
+        float s4[4];
+        dot_part4<DL, SP::LPR>(qr, k + (key * H + h) * D + dofs, H * D, sm_scale, s4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[(kk + i) * RPW + r] = s4[i];  // the LPR lanes of a row store the same value
+          bmax = fmaxf(bmax, s4[i]);
+        }
       }
       rm = fmaxf(rm, bmax);
       rescale = expf(rm - fm);
@@ -221,7 +287,8 @@ __global__ void __launch_bounds__(kRows) attend_kernel(const float* q, const flo
     float lb = 0.0f;
     for (int kk = 0; kk < kTileQ; ++kk) {
       const int64_t key = j * kTileQ + kk;
-      const float s = dot_row<D>(qr, k + (key * H + h) * D, sm_scale);
+      const float s =
+          MODE != 0 ? sc[kk * RPW + r] : dot_part<DL, SP::LPR>(qr, k + (key * H + h) * D + dofs, sm_scale);
       float pw;
       if (MODE == 0) {
         const float p = expf(s - fm);
@@ -237,7 +304,7 @@ __global__ void __launch_bounds__(kRows) attend_kernel(const float* q, const flo
           lb += w;
           const float scaled = on * 256.0f;
           const float pq = e4m3_decode(e4m3_encode(scaled)) * (1.0f / 256.0f);
-          if (p_counts) {
+          if (p_counts && part == 0) {  // once per row
             uf += (pq == 0.0f && scaled != 0.0f) ? 1ull : 0ull;
             cnt += 1;
             const double e = static_cast<double>(pq) - static_cast<double>(on);
@@ -248,9 +315,9 @@ __global__ void __launch_bounds__(kRows) attend_kernel(const float* q, const flo
       }
       if (!kj) continue;
       if (round_p) pw = round_bf16(pw);
-      const float* vrow = v + (key * H + h) * D;
+      const float* vrow = v + (key * H + h) * D + dofs;
 #pragma unroll
-      for (int d = 0; d < D; d += 4) {
+      for (int d = 0; d < DL; d += 4) {
         const float4 v4 = *reinterpret_cast<const float4*>(vrow + d);
         acc[d] = fmaf(pw, v4.x, acc[d]);
         acc[d + 1] = fmaf(pw, v4.y, acc[d + 1]);
@@ -265,14 +332,14 @@ __global__ void __launch_bounds__(kRows) attend_kernel(const float* q, const flo
     }
   }
   const float dn = MODE == 2 ? fmaxf(den, kDenomFloor) : den;
-  float* orow = out + (row * H + h) * D;
+  float* orow = out + (row * H + h) * D + dofs;
 #pragma unroll
-  for (int d = 0; d < D; d += 4) {
+  for (int d = 0; d < DL; d += 4) {
     float4 o;
     o.x = acc[d] / dn; o.y = acc[d + 1] / dn; o.z = acc[d + 2] / dn; o.w = acc[d + 3] / dn;
     *reinterpret_cast<float4*>(orow + d) = o;
   }
-  if (MODE == 2 && dropped) dropped[h * S + row] = drop_l / fmaxf(tot_l, kDenomFloor);
+  if (MODE == 2 && dropped && part == 0) dropped[h * S + row] = drop_l / fmaxf(tot_l, kDenomFloor);
   if (MODE == 2 && p_counts) {
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
@@ -336,12 +403,13 @@ extern "C" int lbfq_blasst_scan(const float* q, const float* k, int64_t S, int64
                      neg_inf);
   hipLaunchKernelGGL(fill_kernel, dim3(static_cast<unsigned>((nt + 255) / 256)), dim3(256), 0, st, tile_bmax, nt,
                      neg_inf);
-  const dim3 grid(static_cast<unsigned>(S / kRows), static_cast<unsigned>(H));
   if (D == 128)
-    hipLaunchKernelGGL(scan_kernel<128>, grid, dim3(kRows), 0, st, q, k, S, H, sm_scale, final_max, tile_margin,
+    hipLaunchKernelGGL(scan_kernel<128>, dim3(static_cast<unsigned>(S / Split<128>::RPW), static_cast<unsigned>(H)),
+                       dim3(64), 0, st, q, k, S, H, sm_scale, final_max, tile_margin,
                        tile_bmax);
   else
-    hipLaunchKernelGGL(scan_kernel<64>, grid, dim3(kRows), 0, st, q, k, S, H, sm_scale, final_max, tile_margin,
+    hipLaunchKernelGGL(scan_kernel<64>, dim3(static_cast<unsigned>(S / Split<64>::RPW), static_cast<unsigned>(H)),
+                       dim3(64), 0, st, q, k, S, H, sm_scale, final_max, tile_margin,
                        tile_bmax);
   LBFQ_LAUNCH_CHECK("blasst_scan");
   return 0;
@@ -369,11 +437,11 @@ extern "C" int lbfq_blasst_attend(const lbfq_blasst_attend_params* p, lbfq_strea
   LBFQ_CHECK_ARG(p->mode == 2 || (!p->keep && !p->dropped && !p->p_counts),
                  "blasst_attend: keep masks, dropped mass and P statistics need mode 2");
   LBFQ_CHECK_ARG(!p->p_counts || p->p_sqerr, "blasst_attend: p_counts needs p_sqerr");
-  const dim3 grid(static_cast<unsigned>(p->S / kRows), static_cast<unsigned>(p->H));
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto* pc = reinterpret_cast<unsigned long long*>(p->p_counts);
 #define LBFQ_ATT(DD, MM)                                                                                          \
-  hipLaunchKernelGGL((attend_kernel<DD, MM>), grid, dim3(kRows), 0, st, p->q, p->k, p->v, p->S, p->H, p->sm_scale, \
+  hipLaunchKernelGGL((attend_kernel<DD, MM>), dim3(static_cast<unsigned>(p->S / Split<DD>::RPW),                 \
+                     static_cast<unsigned>(p->H)), dim3(64), 0, st, p->q, p->k, p->v, p->S, p->H, p->sm_scale, \
                      p->round_p_bf16, p->final_max, p->keep, p->out, p->dropped, pc, p->p_sqerr)
   if (p->D == 128) {
     if (p->mode == 0) LBFQ_ATT(128, 0);
