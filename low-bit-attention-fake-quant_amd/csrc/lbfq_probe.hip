@@ -111,23 +111,31 @@ __device__ __forceinline__ v8i_t load_operand(const uint8_t* row, int hh, int g)
 // u = (q . k) * sq * sk * sm_scale * log2(e) + bias.  Per tile and row the
 // update rule of the reference diagnostic is applied (thresholds in log2
 // units), the tile's p = 2^(u - m) summed into l, and per-row counts kept;
-// lanes of the first half add them into the six 64-bit counters.
+// lanes of the first half add them into the six 64-bit counters.  A
+// workgroup is four waves (128 rows) sharing each K tile through LDS.
 template <int D, bool EST>
 __global__ void __launch_bounds__(256) rowmax_count_kernel(const CountArgs a) {
   constexpr int NH = D / 64;
+  // K tiles (64 keys) staged in LDS and shared by the four waves, double
+  // buffered; rows padded by 16 bytes so that the 32 rows one operand read
+  // touches fall on distinct banks
+  constexpr int KP = D + 16, CPR = D / 16, CPT = 64 * CPR / 256;
+  __shared__ __align__(16) uint8_t kl[2][64 * KP];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 31, g = lane >> 5;
   const int bh = blockIdx.y;
   const int q0 = blockIdx.x * 128 + wave * 32;
-  if (q0 >= a.S) return;  // whole wave past the rows (no barriers in this kernel)
+  // every wave stages tiles and meets the barriers; a wave past the rows
+  // (q0 >= S) reads row S - 1 and counts nothing
   const int qi = q0 + li;
   const bool qvalid = qi < a.S;
-  const uint8_t* qrow = a.q_codes + (static_cast<size_t>(bh) * a.P + (qvalid ? qi : q0)) * D;
+  const int qr = qvalid ? qi : a.S - 1;
+  const uint8_t* qrow = a.q_codes + (static_cast<size_t>(bh) * a.P + qr) * D;
   v8i_t qop[NH];
 #pragma unroll
   for (int hh = 0; hh < NH; ++hh) qop[hh] = load_operand(qrow, hh, g);
-  const float qC = a.sml2 * a.q_scale[bh * a.nqkblk + ((qvalid ? qi : q0) >> a.lg_qkblk)];
-  int grp = (qvalid ? qi : q0) >> a.lg_qgroup;  // qm group of this lane's row
+  const float qC = a.sml2 * a.q_scale[bh * a.nqkblk + (qr >> a.lg_qkblk)];
+  int grp = qr >> a.lg_qgroup;  // qm group of this lane's row
   if (grp >= a.G) grp = a.G - 1;
   const float* brow = a.bias ? a.bias + (static_cast<size_t>(bh) * a.G + grp) * a.P : nullptr;
   const uint8_t* kbase = a.k_codes + static_cast<size_t>(bh) * a.P * D;
@@ -135,16 +143,38 @@ __global__ void __launch_bounds__(256) rowmax_count_kernel(const CountArgs a) {
   float m = EST ? a.rowmax[bh * a.G + grp] : -INFINITY;
   float l = 0.0f, max_seen = -INFINITY;
   int updates = 0, rescales = 0, upward = 0, downward = 0;
-  const int nt = (a.S + 63) / 64;
+  const int nt = (a.S + 63) / 64;  // tile rows stay below the pitch (a multiple of 128 >= S)
+  // thread chunk i: row (tid + 256 i) / CPR, 16-byte column (tid + 256 i) % CPR
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 kreg[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    kreg[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<size_t>(c / CPR) * D + 16 * (c % CPR));
+  }
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    *reinterpret_cast<u32x4*>(&kl[0][(c / CPR) * KP + 16 * (c % CPR)]) = kreg[i];
+  }
+  __syncthreads();
   for (int it = 0; it < nt; ++it) {
     const int key0 = it * 64;
+    {  // the next tile (the last one again after the last), in flight during this one
+      const int knext = it + 1 < nt ? key0 + 64 : key0;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        kreg[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<size_t>(knext + c / CPR) * D + 16 * (c % CPR));
+      }
+    }
     float u[2][16];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       v16f_t c;
 #pragma unroll
       for (int r = 0; r < 16; ++r) c[r] = 0.0f;
-      const uint8_t* krow = kbase + static_cast<size_t>(key0 + 32 * t + li) * D;
+      const uint8_t* krow = &kl[it & 1][(32 * t + li) * KP];
 #pragma unroll
       for (int hh = 0; hh < NH; ++hh)
         c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(load_operand(krow, hh, g), qop[hh], c, 0, 0, 0, 0, 0, 0);
@@ -205,6 +235,13 @@ __global__ void __launch_bounds__(256) rowmax_count_kernel(const CountArgs a) {
     m = m_new;
     updates += adjust ? 1 : 0;
     rescales += rescale ? 1 : 0;
+    // into the buffer every wave finished reading a tile ago (unread after the last tile)
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      *reinterpret_cast<u32x4*>(&kl[(it + 1) & 1][(c / CPR) * KP + 16 * (c % CPR)]) = kreg[i];
+    }
+    __syncthreads();
   }
   // rows of this wave: lanes 0..31 (the second half holds the same rows)
   const bool counted = qvalid && g == 0;

@@ -53,10 +53,10 @@ def test_p_requant_rows_errors(gpu):
         p_requant_rows(torch.zeros(1, 4, 8, device=gpu), sm_scale=1.0, block_n=4)
 
 
-def _counter_case(gpu, seed=0, s=1024, h=2):
+def _counter_case(gpu, seed=0, s=1024, h=2, q_group=256):
     from low_bit_fake_quant.attention import _lazy_preprocess, quantize_operands
     from low_bit_fake_quant.rowmax_counters import counter_config
-    cfg = counter_config(q_kmeans_k=8)
+    cfg = counter_config(q_kmeans_k=8, q_smooth_block=q_group)
     q = cpu_randn(1, s, h, 128, seed=seed + 1)
     k = (cpu_randn(1, s, h, 128, seed=seed + 2).float() * 2.0
          + cpu_randn(1, 1, h, 128, seed=seed + 4).float() * 3.0).to(torch.bfloat16)
@@ -69,9 +69,13 @@ def _counter_case(gpu, seed=0, s=1024, h=2):
 PAIRS = [(8.0, 8.0), (16.0, 32.0), (2.0, 4.0)]
 
 
-def test_rowmax_counts_match_oracle_on_kernel_scores(gpu):
+@pytest.mark.parametrize("s,q_group", [(1024, 256), (320, 64)])
+def test_rowmax_counts_match_oracle_on_kernel_scores(gpu, s, q_group):
+    """Counters equal the oracle's on the kernel's own scores.  S = 320 leaves
+    the last 128-row workgroup with two waves past the rows, which still stage
+    their share of every K tile and meet every barrier but count nothing."""
     from low_bit_fake_quant.rowmax_counters import count_rowmax_updates
-    cfg, q, k, v, ops, sm = _counter_case(gpu)
+    cfg, q, k, v, ops, sm = _counter_case(gpu, s=s, q_group=q_group)
     u2, est2 = oprobe.kernel_scores_log2(ops.q_codes.cpu(), ops.q_scale.cpu(), ops.k_codes.cpu(), ops.k_scale.cpu(),
                                          ops.bias.cpu(), ops.rowmax.cpu(), s=ops.s, qk_block=cfg.fp8_block_size,
                                          q_group=cfg.q_smooth_block_size, sm_scale=sm)
