@@ -166,40 +166,76 @@ __device__ __forceinline__ void dot_part4(const float (&q)[DL], const float* kro
 }
 
 // Pass 1: per row the final max; per (tile, key block) the max over the tile's
-// rows of bmax_j - rm_j and of bmax_j.
+// rows of bmax_j - rm_j and of bmax_j.  A workgroup is one 128-row query tile
+// (128 / (64 / LPR) waves); 32-key slices of K are staged in LDS, double
+// buffered, and every wave reads its key rows from there (the two lane
+// halves of a D = 128 wave read two addresses: broadcast reads).
+constexpr int kScanKeys = 32;  // keys per staged slice
+
 template <int D>
-__global__ void __launch_bounds__(64) scan_kernel(const float* q, const float* k, int64_t S, int64_t H,
-                                                  float sm_scale, float* final_max, uint32_t* tile_margin,
-                                                  uint32_t* tile_bmax) {
+__global__ void __launch_bounds__(256) scan_kernel(const float* q, const float* k, int64_t S, int64_t H,
+                                                   float sm_scale, float* final_max, uint32_t* tile_margin,
+                                                   uint32_t* tile_bmax) {
   using SP = Split<D>;
-  constexpr int DL = SP::DL;
+  constexpr int DL = SP::DL, NWV = kTileQ / SP::RPW, NT = 64 * NWV;
+  constexpr int F4 = kScanKeys * D / 4 / NT;  // float4 per thread per slice
+  __shared__ __align__(16) float ks[2][kScanKeys * D];
   const int64_t h = blockIdx.y;
-  const int r = threadIdx.x % SP::RPW, part = threadIdx.x / SP::RPW;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * SP::RPW + r;
-  const int64_t nb = S / kTileQ, mt = row / kTileQ;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int r = lane % SP::RPW, part = lane / SP::RPW;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kTileQ + wave * SP::RPW + r;
+  const int64_t nb = S / kTileQ, mt = blockIdx.x;
   float qr[DL];
 #pragma unroll
   for (int d = 0; d < DL; d += 4) {
     const float4 v = *reinterpret_cast<const float4*>(q + (row * H + h) * D + part * DL + d);
     qr[d] = v.x; qr[d + 1] = v.y; qr[d + 2] = v.z; qr[d + 3] = v.w;
   }
-  float rm = -INFINITY;
-  for (int64_t j = 0; j < nb; ++j) {
-    float bmax = -INFINITY;
-    for (int kk = 0; kk < kTileQ; kk += 4) {
-      const int64_t key = j * kTileQ + kk;
+  // slice n covers keys [32 n, 32 n + 32); thread chunk i is float4 (tid + NT i)
+  // of the slice, key (tid + NT i) / (D / 4)
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4 kreg[F4];
+  const int64_t nslice = S / kScanKeys;
+#pragma unroll
+  for (int i = 0; i < F4; ++i) {
+    const int c = threadIdx.x + NT * i, kk = c / (D / 4), c4 = c % (D / 4);
+    kreg[i] = *reinterpret_cast<const f32x4*>(k + (static_cast<int64_t>(kk) * H + h) * D + 4 * c4);
+  }
+#pragma unroll
+  for (int i = 0; i < F4; ++i) *reinterpret_cast<f32x4*>(&ks[0][4 * (threadIdx.x + NT * i)]) = kreg[i];
+  __syncthreads();
+  float rm = -INFINITY, bmax = -INFINITY;
+  for (int64_t n = 0; n < nslice; ++n) {
+    {  // slice n + 1 (slice n again after the last), in flight during slice n
+      const int64_t key0 = (n + 1 < nslice ? n + 1 : n) * kScanKeys;
+#pragma unroll
+      for (int i = 0; i < F4; ++i) {
+        const int c = threadIdx.x + NT * i, kk = c / (D / 4), c4 = c % (D / 4);
+        kreg[i] = *reinterpret_cast<const f32x4*>(k + ((key0 + kk) * H + h) * D + 4 * c4);
+      }
+    }
+    const float* kb = &ks[n & 1][part * DL];
+    for (int kk = 0; kk < kScanKeys; kk += 4) {
       float s4[4];
-      dot_part4<DL, SP::LPR>(qr, k + (key * H + h) * D + part * DL, H * D, sm_scale, s4);
+      dot_part4<DL, SP::LPR>(qr, kb + kk * D, D, sm_scale, s4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) bmax = fmaxf(bmax, s4[i]);
     }
-    rm = fmaxf(rm, bmax);
-    const float tm = wave_max(bmax - rm), tb = wave_max(bmax);
-    if (threadIdx.x == 0) {
-      const int64_t o = (h * (S / kTileQ) + mt) * nb + j;
-      atomicMax(tile_margin + o, ordered_bits(tm));
-      atomicMax(tile_bmax + o, ordered_bits(tb));
+    if ((n + 1) % (kTileQ / kScanKeys) == 0) {  // the end of key block j
+      const int64_t j = n / (kTileQ / kScanKeys);
+      rm = fmaxf(rm, bmax);
+      const float tm = wave_max(bmax - rm), tb = wave_max(bmax);
+      if (lane == 0) {
+        const int64_t o = (h * (S / kTileQ) + mt) * nb + j;
+        atomicMax(tile_margin + o, ordered_bits(tm));
+        atomicMax(tile_bmax + o, ordered_bits(tb));
+      }
+      bmax = -INFINITY;
     }
+    // into the buffer every wave finished reading a slice ago (unread after the last)
+#pragma unroll
+    for (int i = 0; i < F4; ++i) *reinterpret_cast<f32x4*>(&ks[(n + 1) & 1][4 * (threadIdx.x + NT * i)]) = kreg[i];
+    __syncthreads();
   }
   if (part == 0) final_max[h * S + row] = rm;
 }
@@ -404,12 +440,12 @@ extern "C" int lbfq_blasst_scan(const float* q, const float* k, int64_t S, int64
   hipLaunchKernelGGL(fill_kernel, dim3(static_cast<unsigned>((nt + 255) / 256)), dim3(256), 0, st, tile_bmax, nt,
                      neg_inf);
   if (D == 128)
-    hipLaunchKernelGGL(scan_kernel<128>, dim3(static_cast<unsigned>(S / Split<128>::RPW), static_cast<unsigned>(H)),
-                       dim3(64), 0, st, q, k, S, H, sm_scale, final_max, tile_margin,
+    hipLaunchKernelGGL(scan_kernel<128>, dim3(static_cast<unsigned>(S / kTileQ), static_cast<unsigned>(H)),
+                       dim3(64 * kTileQ / Split<128>::RPW), 0, st, q, k, S, H, sm_scale, final_max, tile_margin,
                        tile_bmax);
   else
-    hipLaunchKernelGGL(scan_kernel<64>, dim3(static_cast<unsigned>(S / Split<64>::RPW), static_cast<unsigned>(H)),
-                       dim3(64), 0, st, q, k, S, H, sm_scale, final_max, tile_margin,
+    hipLaunchKernelGGL(scan_kernel<64>, dim3(static_cast<unsigned>(S / kTileQ), static_cast<unsigned>(H)),
+                       dim3(64 * kTileQ / Split<64>::RPW), 0, st, q, k, S, H, sm_scale, final_max, tile_margin,
                        tile_bmax);
   LBFQ_LAUNCH_CHECK("blasst_scan");
   return 0;
